@@ -1,0 +1,134 @@
+/*
+ * ttcd.h - plain C ABI of the MI355X (gfx950) dual-window attention and
+ * chunked causal depthwise conv library (libttcd_amd.so).
+ *
+ * Every buffer is a device pointer owned by the caller; the library never
+ * allocates or frees memory. Strides are in elements; the last (head_dim /
+ * channel) dimension must be contiguous. All kernels are launched on the
+ * caller's stream (`stream` is a hipStream_t passed as void*, NULL = the
+ * legacy default stream) and return without synchronising. Functions are
+ * reentrant and thread-safe; the only global state is a thread-local error
+ * message (ttcd_last_error).
+ *
+ * Windows follow flash-attention's window_size=(W-1, 0): key j is visible to
+ * query i iff 0 <= i - j <= W - 1. Softmax is computed in fp32; LSE outputs
+ * are natural-log, fp32, laid out (B, H, T) contiguous.
+ */
+#ifndef TTCD_H_
+#define TTCD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTCD_ABI_VERSION 1
+
+typedef enum ttcd_status {
+  TTCD_OK = 0,
+  TTCD_ERR_INVALID_ARGUMENT = 1, /* bad shape, window, stride, null pointer */
+  TTCD_ERR_UNSUPPORTED = 2,      /* valid request this build does not cover */
+  TTCD_ERR_HIP = 3               /* the HIP runtime reported a launch error */
+} ttcd_status;
+
+typedef enum ttcd_dtype {
+  TTCD_DTYPE_BF16 = 0,
+  TTCD_DTYPE_F16 = 1,
+  TTCD_DTYPE_F32 = 2
+} ttcd_dtype;
+
+/* Human-readable name of a status code. */
+const char* ttcd_status_string(ttcd_status status);
+
+/* Message describing the last error returned on the calling thread. */
+const char* ttcd_last_error(void);
+
+/* TTCD_ABI_VERSION of the loaded library. */
+int ttcd_abi_version(void);
+
+/*
+ * One-pass dual-window causal GQA attention (forward, prefill, Tq == Tk).
+ * Replaces fused_dual_window_attn / _fused_dual_swa_fwd
+ * (profiling/fused_dual_attn.py:244-272, kernel :44-241).
+ *
+ * q: (B, T, Hq, D); k, v: (B, T, Hkv, D); o_t, o_s: (B, T, Hq, D), all of
+ * `dtype` (BF16 or F16), D in {64, 128}, Hq % Hkv == 0, head h reads kv head
+ * h / (Hq / Hkv). *_stride[4] = element strides of (b, t, h, d); d-stride 1.
+ * o_t and o_s share o_stride. window_t >= T (or < 0) means full causal.
+ * Requires 1 <= window_s <= window_t. lse_t / lse_s may be NULL; when given
+ * they receive log(sum_j exp(sm_scale * q.k_j)) over each window, (B, Hq, T).
+ */
+ttcd_status ttcd_dual_window_attn_fwd(
+    const void* q, const void* k, const void* v, void* o_t, void* o_s,
+    float* lse_t, float* lse_s, int B, int T, int Hq, int Hkv, int D,
+    const int64_t q_stride[4], const int64_t k_stride[4],
+    const int64_t v_stride[4], const int64_t o_stride[4], int window_t,
+    int window_s, float sm_scale, ttcd_dtype dtype, void* stream);
+
+/*
+ * Single-band causal GQA attention over keys with band_lo <= i - j < band_hi.
+ * band_lo = 0, band_hi = W is the flash-attention windowed call
+ * (flash_attn_func(..., causal=True, window_size=(W-1, 0)) as called at
+ * profiling/lse_dual_attn.py:22-23); band_lo = WS, band_hi = WT is the far
+ * band of the LSE-combination variant, computed on the unshifted tensors
+ * (replaces the shifted call at profiling/lse_dual_attn.py:27-29 and
+ * :147-149). Rows with an empty band get o = 0 and lse = -inf.
+ * Requires 0 <= band_lo < band_hi; band_hi >= T means unbounded.
+ */
+ttcd_status ttcd_band_attn_fwd(
+    const void* q, const void* k, const void* v, void* o, float* lse, int B,
+    int T, int Hq, int Hkv, int D, const int64_t q_stride[4],
+    const int64_t k_stride[4], const int64_t v_stride[4],
+    const int64_t o_stride[4], int band_lo, int band_hi, float sm_scale,
+    ttcd_dtype dtype, void* stream);
+
+/*
+ * Exact log-sum-exp merge of two attention partials over disjoint key sets.
+ * Replaces _lse_merge_kernel + the o_t[:, :WS] copy of
+ * lse_dual_window_attn_fa3_fast (profiling/lse_dual_attn.py:106-131, :151-159).
+ * Rows t < row_start: o_t = o_s (copied). Rows t >= row_start:
+ *   lt = logaddexp(lse_s, lse_f); o_t = o_s*exp(lse_s-lt) + o_f*exp(lse_f-lt)
+ * in fp32, rounded once to `dtype`. o_s, o_f, o_t: (B, T, H, D) sharing
+ * o_stride; lse_s, lse_f: (B, H, T) contiguous fp32.
+ */
+ttcd_status ttcd_lse_merge_fwd(const void* o_s, const float* lse_s,
+                               const void* o_f, const float* lse_f, void* o_t,
+                               int B, int T, int H, int D, int row_start,
+                               const int64_t o_stride[4], ttcd_dtype dtype,
+                               void* stream);
+
+/*
+ * Chunk-local causal depthwise conv along C on the (N, C, D) layout.
+ * Replaces causal_dwconv_chunked / _causal_dwconv_fwd
+ * (profiling/fused_conv.py:24-61) and IPTTCDMLP._apply_ttt_conv with
+ * ttt_conv_causal=True (custom_models/ipttcd/modeling_ipttcdv9.py:203-211).
+ *   y[n,c,d] = sum_{j=0..K-1} w[d,j] * x[n, c-(K-1)+j, d]  (x = 0 for c < 0)
+ * accumulated in fp32 as acc = fma(x, w, acc) for j = 0..K-1 from acc = +0,
+ * then rounded once (RNE) to x_dtype. x, y: contiguous (N, C, D);
+ * w: contiguous (D, K). 1 <= K <= 64.
+ */
+ttcd_status ttcd_causal_dwconv_chunked_fwd(const void* x, const void* w,
+                                           void* y, int64_t N, int C, int D,
+                                           int K, ttcd_dtype x_dtype,
+                                           ttcd_dtype w_dtype, void* stream);
+
+/*
+ * Host-only schedule check (no GPU work). Replays the attention kernels'
+ * exact tile/phase schedule for one (b, h) slice of length T and adds, for
+ * every (query i, key j) pair the kernel would fold into each output, one
+ * to counts_near[i*T + j] (phase 1: student window, or the whole band of a
+ * single-band call) and counts_far[i*T + j] (phase 2 of the dual kernel:
+ * window_s <= i - j < window_t). Used by tests to prove every in-band pair
+ * is visited exactly once. Set dual = 0 for the single-band schedule, in
+ * which case window_s = band_lo and window_t = band_hi.
+ */
+ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s,
+                                        int window_t, int32_t* counts_near,
+                                        int32_t* counts_far);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTCD_H_ */

@@ -1,0 +1,102 @@
+"""C ABI: the library loads, exports every function include/ttcd.h declares, and
+rejects bad arguments with the documented status before touching the GPU."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from ttcd_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "ttcd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ttcd_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_lists_match_binding():
+    assert _declared() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.ttcd_abi_version() == 1
+
+
+def test_status_strings():
+    lib = _lib.lib()
+    assert lib.ttcd_status_string(0) == b"TTCD_OK"
+    assert lib.ttcd_status_string(1) == b"TTCD_ERR_INVALID_ARGUMENT"
+    assert lib.ttcd_status_string(2) == b"TTCD_ERR_UNSUPPORTED"
+    assert lib.ttcd_status_string(3) == b"TTCD_ERR_HIP"
+
+
+def _attn_call(fn="dual", **over):
+    """Call an attention entry point with fake (never dereferenced) 16-byte aligned
+    pointers; argument checks run before any HIP call."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x10000)
+    st = _lib.strides4([1 * 64 * 4 * 64, 4 * 64, 64, 1])
+    args = dict(B=1, T=64, Hq=4, Hkv=2, D=64, wt=32, ws=16, scale=0.125, dtype=_lib.DTYPE_BF16,
+                qs=st, ks=_lib.strides4([64 * 2 * 64, 2 * 64, 64, 1]), os=st, q=p, o=p)
+    args.update(over)
+    if fn == "dual":
+        return lib.ttcd_dual_window_attn_fwd(
+            args["q"], p, p, args["o"], p, None, None, args["B"], args["T"], args["Hq"],
+            args["Hkv"], args["D"], args["qs"], args["ks"], args["ks"], args["os"], args["wt"],
+            args["ws"], args["scale"], args["dtype"], None)
+    return lib.ttcd_band_attn_fwd(
+        args["q"], p, p, args["o"], None, args["B"], args["T"], args["Hq"], args["Hkv"],
+        args["D"], args["qs"], args["ks"], args["ks"], args["os"], args.get("lo", 0),
+        args.get("hi", 32), args["scale"], args["dtype"], None)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(ws=33), _lib.TTCD_ERR_INVALID_ARGUMENT),          # ws > wt
+    (dict(ws=0), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(Hq=3), _lib.TTCD_ERR_INVALID_ARGUMENT),           # Hq % Hkv
+    (dict(D=96), _lib.TTCD_ERR_UNSUPPORTED),
+    (dict(dtype=_lib.DTYPE_F32), _lib.TTCD_ERR_UNSUPPORTED),
+    (dict(T=0), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(q=None), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(q=ctypes.c_void_p(0x10008)), _lib.TTCD_ERR_UNSUPPORTED),  # misaligned
+    (dict(qs=_lib.strides4([64 * 4 * 64, 4 * 64, 64, 2])), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(qs=_lib.strides4([64 * 4 * 64, 4 * 64 + 4, 64, 1])), _lib.TTCD_ERR_UNSUPPORTED),
+    (dict(scale=0.0), _lib.TTCD_ERR_INVALID_ARGUMENT),
+])
+def test_dual_rejects(over, status):
+    assert _attn_call("dual", **over) == status
+    assert _lib.lib().ttcd_last_error()
+
+
+@pytest.mark.parametrize("lo,hi", [(-1, 4), (5, 5), (7, 3)])
+def test_band_rejects(lo, hi):
+    assert _attn_call("band", lo=lo, hi=hi) == _lib.TTCD_ERR_INVALID_ARGUMENT
+
+
+def test_conv_rejects():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x10000)
+    assert lib.ttcd_causal_dwconv_chunked_fwd(None, p, p, 1, 4, 8, 5, 0, 0, None) == 1
+    assert lib.ttcd_causal_dwconv_chunked_fwd(p, p, p, 1, 4, 8, 0, 0, 0, None) == 1
+    assert lib.ttcd_causal_dwconv_chunked_fwd(p, p, p, 1, 4, 8, 65, 0, 0, None) == 1
+    assert lib.ttcd_causal_dwconv_chunked_fwd(p, p, p, 1, 4, 8, 5, 7, 0, None) == 1
+    # empty tensors are a no-op (no launch)
+    assert lib.ttcd_causal_dwconv_chunked_fwd(p, p, p, 0, 4, 8, 5, 0, 0, None) == 0
+
+
+def test_merge_rejects():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x10000)
+    st = _lib.strides4([64 * 4 * 64, 4 * 64, 64, 1])
+    assert lib.ttcd_lse_merge_fwd(p, p, p, p, None, 1, 64, 4, 64, 0, st, 0, None) == 1
+    assert lib.ttcd_lse_merge_fwd(p, p, p, p, p, 1, 64, 4, 12, 0, st, 0, None) == 2
+    assert lib.ttcd_lse_merge_fwd(p, p, p, p, p, 1, 64, 4, 64, -1, st, 0, None) == 1

@@ -1,0 +1,188 @@
+"""Dual-window attention entry points (host side of the HIP kernels).
+
+Mirrors the reference's Python interface for this path:
+
+* ``fused_dual_window_attn`` - profiling/fused_dual_attn.py:244-272
+* ``lse_dual_window_attn`` / ``_fa3`` / ``_fa3_fast`` -
+  profiling/lse_dual_attn.py:16-39, :74-99, :134-160
+
+plus ``window_attn`` / ``band_attn`` (the single-window flash-attention call
+those files make, ``flash_attn_func(q, k, v, causal=True,
+window_size=(W-1, 0))``) and ``lse_merge``.
+
+Windows follow flash-attention's ``(W-1, 0)`` convention: key j is visible
+to query i iff 0 <= i - j <= W - 1; a window of None or < 0 means full
+causal. The softmax scale is head_dim ** -0.5, as in the reference. All
+calls are forward-only, launch on torch's current stream, allocate only
+their outputs and never synchronise.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_DT = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, fn: str):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or t.dim() != 4:
+            raise ValueError(f"{fn}: {name} must be a 4-D tensor (B, T, H, D)")
+    if q.dtype not in _DT:
+        raise ValueError(f"{fn}: dtype {q.dtype} not supported (bfloat16 or float16)")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"{fn}: q, k, v must share one dtype")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError(f"{fn}: q, k, v must be GPU (HIP) tensors")
+    if not (q.device == k.device == v.device):
+        raise ValueError(f"{fn}: q, k, v must be on one device")
+    B, T, H, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[1] != T or k.shape[3] != D:
+        raise ValueError(f"{fn}: k/v must be (B, T, Hkv, D) matching q {tuple(q.shape)}, "
+                         f"got {tuple(k.shape)} / {tuple(v.shape)}")
+    HK = k.shape[2]
+    if H % HK != 0:
+        raise ValueError(f"{fn}: Hq ({H}) must be a multiple of Hkv ({HK})")
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        raise RuntimeError(f"{fn} is forward-only: autograd / gradient inputs are not supported; "
+                           "call it under torch.no_grad() or torch.inference_mode()")
+    return B, T, H, HK, D
+
+
+def _lse_ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def fused_dual_window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           window_teacher: int, window_student: int, block_n: int = 64,
+                           *, return_lse: bool = False):
+    """Returns (o_teacher, o_student) of one pass over K/V.
+
+    Same call as profiling/fused_dual_attn.py:244: q (B, T, H, D), k/v
+    (B, T, HK, D) bf16/fp16, H % HK == 0; window_teacher None/-1 = full
+    causal; window_student <= window_teacher (AssertionError otherwise).
+    ``block_n`` is accepted for signature compatibility; the gfx950 kernel
+    always sweeps 64-key tiles. Unlike the reference, window_student may be
+    any value >= 1 and teacher == student windows of any alignment are exact.
+    With ``return_lse=True`` also returns (lse_teacher, lse_student), fp32
+    natural-log (B, H, T).
+    """
+    T = q.shape[1]
+    if window_teacher is None or window_teacher < 0:
+        window_teacher = T
+    assert window_student <= window_teacher
+    assert window_student >= 1, "window_student must be >= 1"
+    if int(block_n) <= 0:
+        raise ValueError("block_n must be positive")
+    B, T, H, HK, D = _check_qkv(q, k, v, "fused_dual_window_attn")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    ot = torch.empty_like(q)
+    os_ = torch.empty_like(q)
+    lse_t = lse_s = None
+    if return_lse:
+        lse_t = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
+        lse_s = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
+    L = _lib.lib()
+    _lib.check(L.ttcd_dual_window_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), ot.data_ptr(), os_.data_ptr(),
+        _lse_ptr(lse_t), _lse_ptr(lse_s), B, T, H, HK, D,
+        _lib.strides4(q.stride()), _lib.strides4(k.stride()), _lib.strides4(v.stride()),
+        _lib.strides4(ot.stride()), int(min(window_teacher, 2**31 - 1)),
+        int(min(window_student, 2**31 - 1)), D ** -0.5, _DT[q.dtype], _stream(q.device)))
+    if return_lse:
+        return ot, os_, lse_t, lse_s
+    return ot, os_
+
+
+def band_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, band_lo: int, band_hi: int,
+              *, return_lse: bool = False):
+    """Causal attention over keys j with band_lo <= i - j < band_hi.
+
+    (0, W) is flash_attn_func(q, k, v, causal=True, window_size=(W-1, 0));
+    (WS, WT) is the far band of the LSE variant on unshifted tensors. Rows
+    whose band is empty get o = 0 and lse = -inf.
+    """
+    B, T, H, HK, D = _check_qkv(q, k, v, "band_attn")
+    if band_hi is None or band_hi < 0:
+        band_hi = max(T, band_lo + 1)
+    if not (0 <= band_lo < band_hi):
+        raise ValueError(f"band_attn: need 0 <= band_lo < band_hi, got ({band_lo}, {band_hi})")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, T, device=q.device, dtype=torch.float32) if return_lse else None
+    L = _lib.lib()
+    _lib.check(L.ttcd_band_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), _lse_ptr(lse),
+        B, T, H, HK, D,
+        _lib.strides4(q.stride()), _lib.strides4(k.stride()), _lib.strides4(v.stride()),
+        _lib.strides4(o.stride()), int(min(band_lo, 2**31 - 1)), int(min(band_hi, 2**31 - 1)),
+        D ** -0.5, _DT[q.dtype], _stream(q.device)))
+    return (o, lse) if return_lse else o
+
+
+def window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int | None,
+                *, return_lse: bool = False):
+    """flash_attn_func(q, k, v, causal=True, window_size=(window-1, 0)) on gfx950;
+    window None or < 0 = full causal. The "two separate calls" comparator."""
+    T = q.shape[1]
+    w = T if (window is None or window < 0) else window
+    if w < 1:
+        raise ValueError("window must be >= 1")
+    return band_attn(q, k, v, 0, w, return_lse=return_lse)
+
+
+def lse_merge(o_s: torch.Tensor, lse_s: torch.Tensor, o_f: torch.Tensor, lse_f: torch.Tensor,
+              row_start: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """o_t = o_s*exp(lse_s-lt) + o_f*exp(lse_f-lt), lt = logaddexp(lse_s, lse_f), rows
+    t >= row_start; rows below row_start copy o_s. o_*: (B, T, H, D), lse_*: (B, H, T) fp32.
+    profiling/lse_dual_attn.py:106-131 and :151-159 (o_t[:, :WS] = o_s[:, :WS])."""
+    B, T, H, D = o_s.shape
+    if o_f.shape != o_s.shape or o_f.dtype != o_s.dtype or o_s.dtype not in _DT:
+        raise ValueError("lse_merge: o_s and o_f must share shape and a bf16/fp16 dtype")
+    if lse_s.shape != (B, H, T) or lse_f.shape != (B, H, T):
+        raise ValueError("lse_merge: lse tensors must be (B, H, T)")
+    o_s, o_f = o_s.contiguous(), o_f.contiguous()
+    lse_s = lse_s.float().contiguous()
+    lse_f = lse_f.float().contiguous()
+    o_t = torch.empty_like(o_s) if out is None else out
+    if o_t.shape != o_s.shape or o_t.stride() != o_s.stride():
+        raise ValueError("lse_merge: out must be contiguous like o_s")
+    L = _lib.lib()
+    _lib.check(L.ttcd_lse_merge_fwd(
+        o_s.data_ptr(), lse_s.data_ptr(), o_f.data_ptr(), lse_f.data_ptr(), o_t.data_ptr(),
+        B, T, H, D, int(row_start), _lib.strides4(o_s.stride()), _DT[o_s.dtype],
+        _stream(o_s.device)))
+    return o_t
+
+
+def lse_dual_window_attn(q, k, v, window_teacher: int, window_student: int):
+    """Student = window WS (with LSE); far band [WS, WT) (with LSE); teacher =
+    exact LSE merge. profiling/lse_dual_attn.py:16-39 (flash-attn there, the
+    gfx950 band kernel here). Requires WS < WT (AssertionError otherwise)."""
+    B, T, H, D = q.shape
+    WT = T if (window_teacher is None or window_teacher < 0) else window_teacher
+    WS = window_student
+    assert WS < WT
+    o_s, lse_s = window_attn(q, k, v, WS, return_lse=True)
+    if T <= WS:
+        return o_s, o_s
+    o_f, lse_f = band_attn(q, k, v, WS, WT, return_lse=True)
+    o_t = lse_merge(o_s, lse_s, o_f, lse_f, row_start=WS)
+    return o_t, o_s
+
+
+def lse_dual_window_attn_fa3(q, k, v, window_teacher: int, window_student: int):
+    """profiling/lse_dual_attn.py:74-99 (FA3 flavour). No FA3 on gfx950: the same band
+    kernels serve it, and the far band needs no .contiguous() slice copies."""
+    return lse_dual_window_attn(q, k, v, window_teacher, window_student)
+
+
+def lse_dual_window_attn_fa3_fast(q, k, v, window_teacher: int, window_student: int):
+    """profiling/lse_dual_attn.py:134-160 (two band calls + one-pass merge kernel);
+    the student output is exactly the single-window call's output."""
+    return lse_dual_window_attn(q, k, v, window_teacher, window_student)

@@ -1,0 +1,270 @@
+// api.hip - the extern "C" entry points declared in include/ttcd.h:
+// argument validation (before any HIP call, so every error path is
+// testable without a GPU), status/error reporting, and the host replay of
+// the attention schedule used by the coverage tests.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "internal.h"
+#include "schedule.h"
+#include "ttcd.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+ttcd_status fail(ttcd_status st, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return st;
+}
+
+ttcd_status ok() {
+  g_err[0] = '\0';
+  return TTCD_OK;
+}
+
+ttcd_status from_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(TTCD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks shared by both attention entry points.
+ttcd_status check_attn(const void* q, const void* k, const void* v, const void* o, int B, int T,
+                       int Hq, int Hkv, int D, const int64_t* qs, const int64_t* ks,
+                       const int64_t* vs, const int64_t* os, ttcd_dtype dtype) {
+  if (!q || !k || !v || !o) return fail(TTCD_ERR_INVALID_ARGUMENT, "null tensor pointer");
+  if (!qs || !ks || !vs || !os) return fail(TTCD_ERR_INVALID_ARGUMENT, "null stride array");
+  if (B < 1 || T < 1 || Hq < 1 || Hkv < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "B, T, Hq, Hkv must be >= 1 (got %d, %d, %d, %d)", B,
+                T, Hq, Hkv);
+  if (Hq % Hkv != 0)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "Hq (%d) must be a multiple of Hkv (%d)", Hq, Hkv);
+  if (D != 64 && D != 128)
+    return fail(TTCD_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", D);
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "attention dtype must be bf16 or f16");
+  if (qs[3] != 1 || ks[3] != 1 || vs[3] != 1 || os[3] != 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "head_dim must be contiguous (d-stride 1)");
+  const int64_t* all[4] = {qs, ks, vs, os};
+  for (int t = 0; t < 4; ++t)
+    for (int i = 0; i < 3; ++i)
+      if (all[t][i] % 8 != 0 || all[t][i] < 0)
+        return fail(TTCD_ERR_UNSUPPORTED,
+                    "strides must be non-negative multiples of 8 elements (16-byte rows)");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(TTCD_ERR_UNSUPPORTED, "tensor base pointers must be 16-byte aligned");
+  const int64_t nqb = (T + ttcd::kBlockM - 1) / ttcd::kBlockM;
+  if ((int64_t)B * Hq * nqb > 0x7fffffffLL)
+    return fail(TTCD_ERR_UNSUPPORTED, "grid too large");
+  return TTCD_OK;
+}
+
+ttcd::AttnArgs fill_args(const void* q, const void* k, const void* v, int B, int T, int Hq,
+                         int Hkv, const int64_t* qs, const int64_t* ks, const int64_t* vs,
+                         const int64_t* os, float sm_scale) {
+  ttcd::AttnArgs a = {};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.q_sb = qs[0];
+  a.q_st = qs[1];
+  a.q_sh = qs[2];
+  a.k_sb = ks[0];
+  a.k_st = ks[1];
+  a.k_sh = ks[2];
+  a.v_sb = vs[0];
+  a.v_st = vs[1];
+  a.v_sh = vs[2];
+  a.o_sb = os[0];
+  a.o_st = os[1];
+  a.o_sh = os[2];
+  a.B = B;
+  a.T = T;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.nqb = (T + ttcd::kBlockM - 1) / ttcd::kBlockM;
+  a.c = sm_scale * 1.4426950408889634f;
+  return a;
+}
+
+ttcd::Elem elem(ttcd_dtype d) {
+  return d == TTCD_DTYPE_BF16 ? ttcd::Elem::BF16
+                              : (d == TTCD_DTYPE_F16 ? ttcd::Elem::F16 : ttcd::Elem::F32);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ttcd_status_string(ttcd_status status) {
+  switch (status) {
+    case TTCD_OK: return "TTCD_OK";
+    case TTCD_ERR_INVALID_ARGUMENT: return "TTCD_ERR_INVALID_ARGUMENT";
+    case TTCD_ERR_UNSUPPORTED: return "TTCD_ERR_UNSUPPORTED";
+    case TTCD_ERR_HIP: return "TTCD_ERR_HIP";
+  }
+  return "TTCD_ERR_UNKNOWN";
+}
+
+const char* ttcd_last_error(void) { return g_err; }
+
+int ttcd_abi_version(void) { return TTCD_ABI_VERSION; }
+
+ttcd_status ttcd_dual_window_attn_fwd(const void* q, const void* k, const void* v, void* o_t,
+                                      void* o_s, float* lse_t, float* lse_s, int B, int T,
+                                      int Hq, int Hkv, int D, const int64_t q_stride[4],
+                                      const int64_t k_stride[4], const int64_t v_stride[4],
+                                      const int64_t o_stride[4], int window_t, int window_s,
+                                      float sm_scale, ttcd_dtype dtype, void* stream) {
+  ttcd_status st =
+      check_attn(q, k, v, o_t, B, T, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
+  if (st != TTCD_OK) return st;
+  if (!o_s) return fail(TTCD_ERR_INVALID_ARGUMENT, "null student output pointer");
+  if (!aligned16(o_s)) return fail(TTCD_ERR_UNSUPPORTED, "o_s must be 16-byte aligned");
+  if (window_t < 0) window_t = T;
+  if (window_s < 1) return fail(TTCD_ERR_INVALID_ARGUMENT, "window_s must be >= 1 (got %d)", window_s);
+  if (window_s > window_t)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "window_s (%d) must be <= window_t (%d)", window_s,
+                window_t);
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "sm_scale must be finite and > 0");
+  ttcd::AttnArgs a = fill_args(q, k, v, B, T, Hq, Hkv, q_stride, k_stride, v_stride, o_stride,
+                               sm_scale);
+  a.o_t = o_t;
+  a.o_s = o_s;
+  a.lse_t = lse_t;
+  a.lse_s = lse_s;
+  a.sched = ttcd::make_dual_schedule(T, window_s, window_t);
+  return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
+                  "dual-window attention launch");
+}
+
+ttcd_status ttcd_band_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                               int B, int T, int Hq, int Hkv, int D, const int64_t q_stride[4],
+                               const int64_t k_stride[4], const int64_t v_stride[4],
+                               const int64_t o_stride[4], int band_lo, int band_hi,
+                               float sm_scale, ttcd_dtype dtype, void* stream) {
+  ttcd_status st =
+      check_attn(q, k, v, o, B, T, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
+  if (st != TTCD_OK) return st;
+  if (band_lo < 0 || band_hi <= band_lo)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi (got %d, %d)", band_lo,
+                band_hi);
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "sm_scale must be finite and > 0");
+  ttcd::AttnArgs a = fill_args(q, k, v, B, T, Hq, Hkv, q_stride, k_stride, v_stride, o_stride,
+                               sm_scale);
+  a.o_t = o;
+  a.lse_t = lse;
+  a.sched = ttcd::make_band_schedule(T, band_lo, band_hi);
+  return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
+                  "band attention launch");
+}
+
+ttcd_status ttcd_lse_merge_fwd(const void* o_s, const float* lse_s, const void* o_f,
+                               const float* lse_f, void* o_t, int B, int T, int H, int D,
+                               int row_start, const int64_t o_stride[4], ttcd_dtype dtype,
+                               void* stream) {
+  if (!o_s || !lse_s || !o_f || !lse_f || !o_t || !o_stride)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (B < 1 || T < 1 || H < 1 || D < 8)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "B, T, H must be >= 1 and D >= 8");
+  if (D % 8 != 0) return fail(TTCD_ERR_UNSUPPORTED, "D must be a multiple of 8");
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "merge dtype must be bf16 or f16");
+  if (o_stride[3] != 1) return fail(TTCD_ERR_INVALID_ARGUMENT, "D must be contiguous");
+  for (int i = 0; i < 3; ++i)
+    if (o_stride[i] % 8 != 0 || o_stride[i] < 0)
+      return fail(TTCD_ERR_UNSUPPORTED, "strides must be non-negative multiples of 8");
+  if (!aligned16(o_s) || !aligned16(o_f) || !aligned16(o_t))
+    return fail(TTCD_ERR_UNSUPPORTED, "outputs must be 16-byte aligned");
+  if (row_start < 0) return fail(TTCD_ERR_INVALID_ARGUMENT, "row_start must be >= 0");
+  return from_hip(ttcd::launch_lse_merge(o_s, lse_s, o_f, lse_f, o_t, B, T, H, D, row_start,
+                                         o_stride[0], o_stride[1], o_stride[2], elem(dtype),
+                                         static_cast<hipStream_t>(stream)),
+                  "lse merge launch");
+}
+
+ttcd_status ttcd_causal_dwconv_chunked_fwd(const void* x, const void* w, void* y, int64_t N,
+                                           int C, int D, int K, ttcd_dtype x_dtype,
+                                           ttcd_dtype w_dtype, void* stream) {
+  if (!x || !w || !y) return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (N < 0 || C < 0 || D < 0) return fail(TTCD_ERR_INVALID_ARGUMENT, "negative extent");
+  if (K < 1 || K > 64) return fail(TTCD_ERR_INVALID_ARGUMENT, "kernel size %d not in [1, 64]", K);
+  if ((unsigned)x_dtype > TTCD_DTYPE_F32 || (unsigned)w_dtype > TTCD_DTYPE_F32)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (N == 0 || C == 0 || D == 0) return ok();
+  return from_hip(ttcd::launch_dwconv(x, w, y, N, C, D, K, elem(x_dtype), elem(w_dtype),
+                                      static_cast<hipStream_t>(stream)),
+                  "depthwise conv launch");
+}
+
+ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int window_t,
+                                        int32_t* counts_near, int32_t* counts_far) {
+  using namespace ttcd;
+  if (T < 1 || !counts_near || (dual && !counts_far))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "bad coverage arguments");
+  Schedule sc;
+  if (dual) {
+    if (window_t < 0) window_t = T;
+    if (window_s < 1 || window_s > window_t)
+      return fail(TTCD_ERR_INVALID_ARGUMENT, "need 1 <= window_s <= window_t");
+    sc = make_dual_schedule(T, window_s, window_t);
+  } else {
+    if (window_s < 0 || window_t <= window_s)
+      return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi");
+    sc = make_band_schedule(T, window_s, window_t);
+  }
+  const int nqb = (T + kBlockM - 1) / kBlockM;
+  for (int qb = 0; qb < nqb; ++qb) {
+    const int t0 = qb * kBlockM;
+    const int t_last = (t0 + kBlockM < T ? t0 + kBlockM : T) - 1;
+    int n_hi, n_lo;
+    if (!sc.wg_range(t0, t_last, &n_hi, &n_lo)) continue;
+    for (int w = 0; w < kWaves; ++w) {
+      const int r0 = t0 + w * kWaveRows;
+      if (r0 >= T) continue;
+      bool done1 = false;  // phase 1 finished (student output emitted)
+      for (int n = n_hi; n >= n_lo; --n) {
+        const int j0 = sc.tile_start(n);
+        const bool in1 = wave_touches(r0, sc.p1, j0);
+        const bool in2 = sc.dual && wave_touches(r0, sc.p2, j0);
+        for (int phase = 1; phase <= 2; ++phase) {
+          const bool in = phase == 1 ? in1 : in2;
+          if (!in) continue;
+          const Band band = phase == 1 ? sc.p1 : sc.p2;
+          if (phase == 1 && done1)
+            return fail(TTCD_ERR_UNSUPPORTED, "schedule error: phase-1 tile after emit (r0=%d n=%d)",
+                        r0, n);
+          if (phase == 2 && !done1 && !(in1 && wave_last(r0, sc.p1, j0)))
+            return fail(TTCD_ERR_UNSUPPORTED,
+                        "schedule error: phase-2 tile before student emit (r0=%d n=%d)", r0, n);
+          const bool full = wave_full(r0, band, j0);
+          for (int i = r0; i < r0 + kWaveRows && i < T; ++i) {
+            for (int j = j0; j < j0 + kBlockN; ++j) {
+              const bool inc = full || visible(i, j, band, T);
+              if (!inc) continue;
+              if (j < 0 || j >= T)
+                return fail(TTCD_ERR_UNSUPPORTED, "schedule error: key %d out of range", j);
+              int32_t* cnt = phase == 1 ? counts_near : counts_far;
+              cnt[(int64_t)i * T + j] += 1;
+            }
+          }
+          if (phase == 1 && wave_last(r0, sc.p1, j0)) done1 = true;
+        }
+      }
+    }
+  }
+  return ok();
+}
+
+}  // extern "C"

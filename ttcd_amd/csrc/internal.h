@@ -1,0 +1,43 @@
+// internal.h - launcher interface between the C ABI (api.hip) and the
+// gfx950 kernels (attn.hip, conv.hip, merge.hip). Not part of the ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "schedule.h"
+
+namespace ttcd {
+
+enum class Elem { BF16 = 0, F16 = 1, F32 = 2 };
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o_t;      // final output (teacher for the dual kernel, band output otherwise)
+  void* o_s;      // student output (dual kernel only)
+  float* lse_t;   // optional (B, Hq, T)
+  float* lse_s;   // optional (B, Hq, T), dual kernel only
+  int64_t q_sb, q_st, q_sh;
+  int64_t k_sb, k_st, k_sh;
+  int64_t v_sb, v_st, v_sh;
+  int64_t o_sb, o_st, o_sh;
+  int B, T, Hq, Hkv, G;
+  int nqb;        // query tiles of kBlockM tokens per (b, h)
+  float c;        // sm_scale * log2(e)
+  Schedule sched;
+};
+
+// Launch the dual-window (sched.dual == 1) or single-band kernel.
+hipError_t launch_attn(const AttnArgs& a, int D, Elem dtype, hipStream_t stream);
+
+hipError_t launch_dwconv(const void* x, const void* w, void* y, int64_t N, int C,
+                         int D, int K, Elem xt, Elem wt, hipStream_t stream);
+
+hipError_t launch_lse_merge(const void* o_s, const float* lse_s, const void* o_f,
+                            const float* lse_f, void* o_t, int B, int T, int H,
+                            int D, int row_start, int64_t sb, int64_t st,
+                            int64_t sh, Elem dtype, hipStream_t stream);
+
+}  // namespace ttcd
