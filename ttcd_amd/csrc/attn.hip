@@ -39,6 +39,10 @@
 #include "internal.h"
 #include "schedule.h"
 
+#ifndef TTCD_WAVES_PER_EU
+#define TTCD_WAVES_PER_EU 2
+#endif
+
 namespace ttcd {
 namespace {
 
@@ -83,23 +87,22 @@ __device__ __forceinline__ int xcd_remap(int g, int total) {
 
 template <int D>
 struct Geo {
-  static constexpr int KSTR = D + 8;        // K tile row stride (elements)
-  static constexpr int VSTR = kBlockN + 8;  // V^T tile row stride (elements)
-  static constexpr int K_ELEMS = kBlockN * KSTR;
+  static constexpr int CPR = D / 8;          // 16-byte chunks per K row
+  static constexpr int VSTR = kBlockN + 8;   // V^T tile row stride (elements)
+  static constexpr int K_ELEMS = kBlockN * D;  // K tile, rows unpadded, chunks XOR-swizzled
   static constexpr int V_ELEMS = D * VSTR;
   static constexpr int STAGE = K_ELEMS + V_ELEMS;
   static constexpr int DK = D / 16;  // MFMA k-steps of S^T = K Q^T
   static constexpr int DT = D / 32;  // 32-row d tiles of O^T
   static constexpr int NTH = kWaves * 64;
-  static constexpr int KCH = kBlockN * (D / 8) / NTH;  // 16-byte K chunks per thread
-  static constexpr int VU = (kBlockN / 2) * (D / 8) / NTH;  // (2 keys x 8 d) V units per thread
-  static_assert(KCH * NTH == kBlockN * (D / 8), "K tile must split evenly");
-  static_assert(VU * NTH == (kBlockN / 2) * (D / 8), "V tile must split evenly");
+  static constexpr int KDMA = kBlockN * CPR / NTH;          // direct K loads per thread
+  static constexpr int VU = (kBlockN / 2) * CPR / NTH;      // (2 keys x 8 d) V units per thread
+  static_assert(KDMA * NTH == kBlockN * CPR, "K tile must split evenly");
+  static_assert(VU * NTH == (kBlockN / 2) * CPR, "V tile must split evenly");
 };
 
 template <int D>
-struct StageRegs {
-  u32x4 k[Geo<D>::KCH];
+struct VStage {
   u32x4 va[Geo<D>::VU];
   u32x4 vb[Geo<D>::VU];
 };
@@ -111,44 +114,54 @@ __device__ __forceinline__ int vt_pos(int kk) {
   return (kk & ~15) | (kk & 3) | ((kk >> 3) & 1) << 2 | ((kk >> 2) & 1) << 3;
 }
 
+// K tile: global -> LDS without registers (global_load_lds_dwordx4). Each wave
+// instruction writes 64 consecutive 16-byte LDS slots; slot s of row r holds
+// global chunk s ^ (r mod CPR), which makes the 16 lanes of an MFMA operand
+// read (16 rows, one chunk) hit 16 distinct bank groups. Rows outside [0, T)
+// are clamped to a valid row; every score they produce is masked.
 template <int D, typename T>
-__device__ __forceinline__ void load_tile(StageRegs<D>& r, const T* kp, const T* vp,
-                                          int64_t k_st, int64_t v_st, int j0, int T_,
-                                          int tid) {
+__device__ __forceinline__ void issue_k_tile(T* ks, const T* kp, int64_t k_st, int j0, int T_,
+                                             int wave, int lane) {
   using G = Geo<D>;
-  constexpr int CPR = D / 8;  // 16-byte chunks per key row
 #pragma unroll
-  for (int i = 0; i < G::KCH; ++i) {
-    const int c = tid + i * G::NTH;
-    const int j = j0 + c / CPR;
-    const int dch = c % CPR;
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (j >= 0 && j < T_) val = *reinterpret_cast<const u32x4*>(kp + (int64_t)j * k_st + dch * 8);
-    r.k[i] = val;
+  for (int i = 0; i < G::KDMA; ++i) {
+    const int base = (i * kWaves + wave) * 64;  // first chunk slot of this instruction
+    const int slot = base + lane;
+    const int row = slot / G::CPR;
+    const int chunk = (slot % G::CPR) ^ (row % G::CPR);
+    int j = j0 + row;
+    j = j < 0 ? 0 : (j >= T_ ? T_ - 1 : j);
+    const T* src = kp + (int64_t)j * k_st + chunk * 8;
+    __builtin_amdgcn_global_load_lds(
+        (const __attribute__((address_space(1))) void*)src,
+        (__attribute__((address_space(3))) void*)(ks + base * 8), 16, 0, 0);
   }
+}
+
+template <int D, typename T>
+__device__ __forceinline__ void load_v_tile(VStage<D>& r, const T* vp, int64_t v_st, int j0,
+                                            int T_, int tid) {
+  using G = Geo<D>;
 #pragma unroll
   for (int i = 0; i < G::VU; ++i) {
     const int u = tid + i * G::NTH;
     const int ja = j0 + 2 * (u & 31);
     const int dch = u >> 5;
-    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-    if (ja >= 0 && ja < T_) a = *reinterpret_cast<const u32x4*>(vp + (int64_t)ja * v_st + dch * 8);
-    if (ja + 1 >= 0 && ja + 1 < T_)
-      b = *reinterpret_cast<const u32x4*>(vp + (int64_t)(ja + 1) * v_st + dch * 8);
-    r.va[i] = a;
-    r.vb[i] = b;
+    // unconditional loads from clamped rows, zeroed outside [0, T): no branches
+    const int jca = ja < 0 ? 0 : (ja >= T_ ? T_ - 1 : ja);
+    const int jcb = ja + 1 < 0 ? 0 : (ja + 1 >= T_ ? T_ - 1 : ja + 1);
+    const u32x4 a = *reinterpret_cast<const u32x4*>(vp + (int64_t)jca * v_st + dch * 8);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(vp + (int64_t)jcb * v_st + dch * 8);
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    r.va[i] = (ja >= 0 && ja < T_) ? a : z;
+    r.vb[i] = (ja + 1 >= 0 && ja + 1 < T_) ? b : z;
   }
 }
 
+// V tile registers -> LDS transposed (V^T rows = d, key positions vt_pos).
 template <int D, typename T>
-__device__ __forceinline__ void store_tile(const StageRegs<D>& r, T* ks, T* vt, int tid) {
+__device__ __forceinline__ void store_v_tile(const VStage<D>& r, T* vt, int tid) {
   using G = Geo<D>;
-  constexpr int CPR = D / 8;
-#pragma unroll
-  for (int i = 0; i < G::KCH; ++i) {
-    const int c = tid + i * G::NTH;
-    *reinterpret_cast<u32x4*>(ks + (c / CPR) * G::KSTR + (c % CPR) * 8) = r.k[i];
-  }
 #pragma unroll
   for (int i = 0; i < G::VU; ++i) {
     const int u = tid + i * G::NTH;
@@ -158,12 +171,29 @@ __device__ __forceinline__ void store_tile(const StageRegs<D>& r, T* ks, T* vt, 
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint32_t a = r.va[i][e], b = r.vb[i][e];
-      const uint32_t lo = (a & 0xffffu) | (b << 16);          // d = 8*dch + 2e
-      const uint32_t hi = (a >> 16) | (b & 0xffff0000u);      // d = 8*dch + 2e + 1
+      const uint32_t lo = (a & 0xffffu) | (b << 16);      // d = 8*dch + 2e
+      const uint32_t hi = (a >> 16) | (b & 0xffff0000u);  // d = 8*dch + 2e + 1
       *reinterpret_cast<uint32_t*>(base + (2 * e) * G::VSTR) = lo;
       *reinterpret_cast<uint32_t*>(base + (2 * e + 1) * G::VSTR) = hi;
     }
   }
+}
+
+// Scheduling masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
+// Interleave N LDS operand reads with the N MFMAs that consume them, two
+// reads in flight: r r (M r)* M M.
+template <int N>
+__device__ __forceinline__ void pipeline_reads_with_mfma() {
+  __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+#pragma unroll
+  for (int i = 0; i < N - 2; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
 }
 
 // S^T (64 keys x 32 queries) of the current tile: two 32x32 fp32 tiles.
@@ -173,75 +203,100 @@ __device__ __forceinline__ void compute_scores(f32x16 (&s)[2], const T* ks,
                                                int lane) {
   using G = Geo<D>;
   using v8 = typename VecT<T>::v8;
-  const T* base = ks + (lane & 31) * G::KSTR + (lane >> 5) * 8;
+  constexpr int N = 2 * G::DK;
+  const int r = lane & 31;
+  // Chunk 2*ks + half of row r lives in slot (2*ks) ^ y, y = half ^ (r mod CPR).
+  // Row bases are multiples of the row size, so the byte offset of every
+  // (kt, ks) operand is one XOR of a per-lane base with a constant (plus the
+  // kt row block). The empty asm keeps the compiler from hoisting all DK
+  // XOR results out of the tile loop into DK live registers.
+  uint32_t xbase = (uint32_t)(r * D * 2) | (uint32_t)(((lane >> 5) ^ (r % G::CPR)) << 4);
+  asm volatile("" : "+v"(xbase));
+  const char* kb = reinterpret_cast<const char*>(ks);
+  v8 a[N];
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    f32x16 acc = {};
-#pragma unroll
-    for (int kst = 0; kst < G::DK; ++kst) {
-      const v8 a = *reinterpret_cast<const v8*>(base + kt * 32 * G::KSTR + kst * 16);
-      acc = mfma32(a, qf[kst], acc);
-    }
-    s[kt] = acc;
+  for (int i = 0; i < N; ++i) {
+    const uint32_t off = (xbase ^ (uint32_t)((i % G::DK) << 5)) + (i / G::DK) * 32 * D * 2;
+    a[i] = *reinterpret_cast<const v8*>(kb + off);
   }
+  s[0] = f32x16{};
+  s[1] = f32x16{};
+#pragma unroll
+  for (int i = 0; i < N; ++i) s[i / G::DK] = mfma32(a[i], qf[i % G::DK], s[i / G::DK]);
+  pipeline_reads_with_mfma<N>();
 }
 
+// Lazy online-softmax rescale: the running max used for exp2 is only moved
+// when some row's true max exceeds it by more than 2^kRescaleLog2 (so p stays
+// <= 256 and l, O^T cannot overflow). Softmax is invariant to the reference
+// max, so results are the same up to rounding, and the O^T rescale (a VALU
+// pass over the whole accumulator) leaves the common path: with the
+// diagonal tile first, rows almost never raise their max by 2^8 later.
+constexpr float kRescaleLog2 = 8.0f;
+
 // One online-softmax step of band {lo, hi} over the tile starting at key j0:
-// masks (if MASK), updates the running max m / per-lane partial sum l,
-// rescales O^T and accumulates P^T through V^T.
-template <bool MASK, int D, typename T>
-__device__ __forceinline__ void softmax_pv(const f32x16 (&s)[2], f32x16 (&o)[Geo<D>::DT],
-                                           float& m, float& l, float c, const T* vt,
-                                           int lane, int qrow, int j0, int T_, Band band) {
+// masks S in place (if the tile is not entirely inside the band), updates the
+// running max m / per-lane partial sum l, rescales O^T when needed and
+// accumulates P^T through V^T.
+template <int D, typename T>
+__device__ __forceinline__ void softmax_pv(f32x16 (&s)[2], f32x16 (&o)[Geo<D>::DT], float& m,
+                                           float& l, float c, const T* vt, int lane,
+                                           bool need_mask, int qrow, int j0, int T_, Band band) {
   using G = Geo<D>;
   using v8 = typename VecT<T>::v8;
   const int half = lane >> 5;
-  float sv[32];
-  float mx = -INFINITY;
+  if (need_mask) {
+    const int jb = j0 + 4 * half;
+    const unsigned width = (unsigned)(band.hi - band.lo);
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float x = s[kt][i];
-      if (MASK) {
-        const int j = j0 + kt * 32 + 8 * (i >> 2) + 4 * half + (i & 3);
-        const int d = qrow - j;
-        const bool ok = (unsigned)(d - band.lo) < (unsigned)(band.hi - band.lo) &&
-                        (unsigned)j < (unsigned)T_;
-        x = ok ? x : -INFINITY;
+      for (int i = 0; i < 16; ++i) {
+        const int j = jb + kt * 32 + 8 * (i >> 2) + (i & 3);
+        const bool ok = (unsigned)(qrow - j - band.lo) < width && (unsigned)j < (unsigned)T_;
+        s[kt][i] = ok ? s[kt][i] : -INFINITY;
       }
-      sv[kt * 16 + i] = x;
-      mx = fmaxf(mx, x);
     }
   }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
   mx = fmaxf(mx, __shfl_xor(mx, 32));
   const float m_new = fmaxf(m, mx);
-  const float mc = (m_new == -INFINITY) ? 0.f : m_new * c;
-  const float alpha = fast_exp2(fmaf(m, c, -mc));
+  // m = -inf and a finite m_new give +inf (rescale); both -inf give NaN (no rescale)
+  const bool grow = (m_new - m) * c > kRescaleLog2;
+  if (__any(grow)) {
+    const float mc_new = (m_new == -INFINITY) ? 0.f : m_new * c;
+    const float alpha = fast_exp2(fmaf(m, c, -mc_new));
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt) o[dt] *= alpha;
+    m = m_new;
+  }
+  const float mc = (m == -INFINITY) ? 0.f : m * c;
   float psum = 0.f;
   v8 pf[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float p = fast_exp2(fmaf(sv[ks * 8 + e], c, -mc));
+      const float p = fast_exp2(fmaf(s[ks >> 1][(ks & 1) * 8 + e], c, -mc));
       psum += p;
       pf[ks][e] = static_cast<T>(p);
     }
   }
-  l = fmaf(l, alpha, psum);
-  m = m_new;
-#pragma unroll
-  for (int dt = 0; dt < G::DT; ++dt) o[dt] *= alpha;
+  l += psum;
+  constexpr int N = 4 * G::DT;
   const T* base = vt + (lane & 31) * G::VSTR + half * 8;
+  v8 b[N];
 #pragma unroll
-  for (int dt = 0; dt < G::DT; ++dt) {
+  for (int i = 0; i < N; ++i)
+    b[i] = *reinterpret_cast<const v8*>(base + (i >> 2) * 32 * G::VSTR + (i & 3) * 16);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const v8 a = *reinterpret_cast<const v8*>(base + dt * 32 * G::VSTR + ks * 16);
-      o[dt] = mfma32(a, pf[ks], o[dt]);
-    }
-  }
+  for (int i = 0; i < N; ++i) o[i >> 2] = mfma32(b[i], pf[i & 3], o[i >> 2]);
+  pipeline_reads_with_mfma<N>();
 }
 
 // Normalise and store one output (and its LSE) from the O^T accumulator.
@@ -271,17 +326,9 @@ __device__ __forceinline__ void emit(const f32x16 (&o)[Geo<D>::DT], float m, flo
   }
 }
 
-// D=64 fits two waves per SIMD (<= 256 VGPRs); D=128 holds a 64-register
-// O^T accumulator plus 32 registers of Q^T and takes one wave per SIMD with
-// the full 512-register file.
-template <int D>
-struct Occ {
-  static constexpr int waves = D == 64 ? 2 : 1;
-};
-
 template <int D, typename T, bool DUAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256),
-                          amdgpu_waves_per_eu(Occ<D>::waves, Occ<D>::waves)))
+                          amdgpu_waves_per_eu(TTCD_WAVES_PER_EU, TTCD_WAVES_PER_EU)))
 void attn_fwd_kernel(AttnArgs a) {
   using G = Geo<D>;
   using v8 = typename VecT<T>::v8;
@@ -340,11 +387,14 @@ void attn_fwd_kernel(AttnArgs a) {
     n_lo = 1;
   }
 
-  StageRegs<D> sr;
+  VStage<D> vr;
   if (n_hi >= n_lo) {
-    load_tile<D, T>(sr, kp, vp, a.k_st, a.v_st, sc.tile_start(n_hi), T_, tid);
-    store_tile<D, T>(sr, smem, smem + G::K_ELEMS, tid);
+    const int j0 = sc.tile_start(n_hi);
+    issue_k_tile<D, T>(smem, kp, a.k_st, j0, T_, wave, lane);
+    load_v_tile<D, T>(vr, vp, a.v_st, j0, T_, tid);
+    store_v_tile<D, T>(vr, smem + G::K_ELEMS, tid);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
   for (int n = n_hi, it = 0; n >= n_lo; --n, ++it) {
@@ -352,34 +402,34 @@ void attn_fwd_kernel(AttnArgs a) {
     T* vt = ks + G::K_ELEMS;
     T* nks = smem + ((it + 1) & 1) * G::STAGE;
     const bool has_next = n - 1 >= n_lo;
-    if (has_next) load_tile<D, T>(sr, kp, vp, a.k_st, a.v_st, sc.tile_start(n - 1), T_, tid);
+    if (has_next) {
+      const int jn = sc.tile_start(n - 1);
+      issue_k_tile<D, T>(nks, kp, a.k_st, jn, T_, wave, lane);
+      load_v_tile<D, T>(vr, vp, a.v_st, jn, T_, tid);
+    }
 
     const int j0 = sc.tile_start(n);
     if (wave_valid) {
       const bool in1 = wave_touches(r0, sc.p1, j0);
       const bool in2 = DUAL && wave_touches(r0, sc.p2, j0);
-      if (in1 || in2) {
+      // At most two passes over the tile: phase 1 then (dual kernel, mixed
+      // tile only) phase 2, which recomputes S rather than keeping a copy.
+      int phase = in1 ? 1 : (in2 ? 2 : 0);
+      while (phase != 0) {
+        const Band band = phase == 1 ? sc.p1 : sc.p2;
         f32x16 s[2];
         compute_scores<D, T>(s, ks, qf, lane);
-        if (in1) {
-          if (wave_full(r0, sc.p1, j0))
-            softmax_pv<false, D, T>(s, o, m, l, a.c, vt, lane, qrow, j0, T_, sc.p1);
-          else
-            softmax_pv<true, D, T>(s, o, m, l, a.c, vt, lane, qrow, j0, T_, sc.p1);
-          if (DUAL && wave_last(r0, sc.p1, j0)) {
-            emit<D, T>(o, m, l, a.c, os, a.o_st, lse_s, qrow, T_, lane);
-            emitted_s = true;
-          }
+        softmax_pv<D, T>(s, o, m, l, a.c, vt, lane, !wave_full(r0, band, j0), qrow, j0, T_,
+                         band);
+        if (DUAL && phase == 1 && wave_last(r0, sc.p1, j0)) {
+          emit<D, T>(o, m, l, a.c, os, a.o_st, lse_s, qrow, T_, lane);
+          emitted_s = true;
         }
-        if (DUAL && in2) {
-          if (wave_full(r0, sc.p2, j0))
-            softmax_pv<false, D, T>(s, o, m, l, a.c, vt, lane, qrow, j0, T_, sc.p2);
-          else
-            softmax_pv<true, D, T>(s, o, m, l, a.c, vt, lane, qrow, j0, T_, sc.p2);
-        }
+        phase = (DUAL && phase == 1 && in2) ? 2 : 0;
       }
     }
-    if (has_next) store_tile<D, T>(sr, nks, nks + G::K_ELEMS, tid);
+    if (has_next) store_v_tile<D, T>(vr, nks + G::K_ELEMS, tid);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
 
