@@ -149,6 +149,45 @@ def numerics_report() -> dict:
     return out
 
 
+def profile_one(args) -> int:
+    """One workload, `--steps` timed launches after `--warmup`, for rocprofv3 runs.
+    'copy' is a plain device-to-device copy of 1 GiB (the known-size kernel used to
+    calibrate the FETCH_SIZE / WRITE_SIZE counters)."""
+    import torch
+    from oracle import attn_ref, conv_ref
+    from ttcd_amd import causal_dwconv_x, fused_dual_window_attn, lse_dual_window_attn, window_attn
+
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    B, T, H, HK, D, wt, ws = (cfg[k] for k in ("B", "T", "Hq", "Hkv", "D", "wt", "ws"))
+    gen = torch.Generator(device=dev).manual_seed(0)
+    if args.only == "copy":
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        fn, work, unit = (lambda: dst.copy_(src)), float(1 << 31), "GB/s"
+    elif args.only == "conv":
+        x = torch.randn(1, 16, 4096, 3072, device=dev, dtype=torch.bfloat16, generator=gen)
+        w = torch.randn(3072, 5, device=dev, dtype=torch.bfloat16, generator=gen)
+        fn, work, unit = (lambda: causal_dwconv_x(x, w)), conv_ref.conv_bytes(16, 4096, 3072, 5), "GB/s"
+    else:
+        q = torch.randn(B, T, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        k = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        v = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        work, unit = attn_ref.attn_flops(B, H, D, T, wt), "TFLOP/s"
+        if args.only == "fused":
+            fn = lambda: fused_dual_window_attn(q, k, v, wt, ws, return_lse=True)  # noqa: E731
+        elif args.only == "band":
+            fn = lambda: window_attn(q, k, v, wt)  # noqa: E731
+        else:
+            fn = lambda: lse_dual_window_attn(q, k, v, wt, ws)  # noqa: E731
+    with torch.inference_mode():
+        ms = time_gpu(fn, args.steps, args.warmup)
+    rate = work / (ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    print(json.dumps({"only": args.only, "config": args.config, "ms": ms, "rate": rate,
+                      "unit": unit, "steps": args.steps}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -159,6 +198,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-numerics", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--only", choices=["fused", "band", "lse", "conv", "copy"],
+                    help="profiling mode: run one workload --steps times and print its timing")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -170,6 +211,9 @@ def main() -> int:
     from oracle import attn_ref, conv_ref
     from ttcd_amd import (causal_dwconv_x, fused_dual_window_attn, lse_dual_window_attn,
                           window_attn)
+
+    if args.only:
+        return profile_one(args)
 
     cfg = CONFIGS[args.config]
     B, T, H, HK, D, wt, ws = (cfg[k] for k in ("B", "T", "Hq", "Hkv", "D", "wt", "ws"))

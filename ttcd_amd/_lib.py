@@ -12,7 +12,8 @@ import os
 import threading
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_PKG_DIR, "lib", "libttcd_amd.so")
+# TTCD_AMD_LIB overrides the library path (e.g. to A/B two builds of the kernels).
+LIB_PATH = os.environ.get("TTCD_AMD_LIB") or os.path.join(_PKG_DIR, "lib", "libttcd_amd.so")
 
 TTCD_OK = 0
 TTCD_ERR_INVALID_ARGUMENT = 1

@@ -59,25 +59,29 @@ def _run(cmd: list[str], verbose: bool) -> None:
             print("\n".join(lines), flush=True)
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile every HIP source for gfx950 and link the shared library."""
+def build(verbose: bool = False, jobs: int | None = None, out: str | None = None,
+          defines: tuple[str, ...] = ()) -> str:
+    """Compile every HIP source for gfx950 and link the shared library (to `out`,
+    default ttcd_amd/lib/libttcd_amd.so; `defines` are extra -D flags)."""
     hipcc = _hipcc()
-    os.makedirs(BUILD_DIR, exist_ok=True)
-    os.makedirs(LIB_DIR, exist_ok=True)
+    out = out or LIB_PATH
+    build_dir = BUILD_DIR if out == LIB_PATH else out + ".objs"
+    os.makedirs(build_dir, exist_ok=True)
+    os.makedirs(os.path.dirname(out), exist_ok=True)
     objs = []
     cmds = []
     for src in SOURCES:
-        obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
+        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, "-I", INCLUDE, "-I", CSRC, "-c",
-                     os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIPCC_FLAGS, *[f"-D{d}" for d in defines], "-I", INCLUDE, "-I",
+                     CSRC, "-c", os.path.join(CSRC, src), "-o", obj])
     jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 4) // 2))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
-    tmp = LIB_PATH + ".tmp"
+    tmp = out + ".tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

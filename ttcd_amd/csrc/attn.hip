@@ -42,6 +42,9 @@
 #ifndef TTCD_WAVES_PER_EU
 #define TTCD_WAVES_PER_EU 2
 #endif
+#ifndef TTCD_INTERLEAVE_PV
+#define TTCD_INTERLEAVE_PV 1
+#endif
 
 namespace ttcd {
 namespace {
@@ -114,24 +117,59 @@ __device__ __forceinline__ int vt_pos(int kk) {
   return (kk & ~15) | (kk & 3) | ((kk >> 3) & 1) << 2 | ((kk >> 2) & 1) << 3;
 }
 
+// Per-thread byte offsets of this thread's tile loads relative to the tile's
+// first key row; computed once, so a tile costs one scalar base update.
+template <int D>
+struct LoadPlan {
+  uint32_t k_off[Geo<D>::KDMA];  // K chunk this lane moves per direct load
+  int k_row[Geo<D>::KDMA];
+  uint32_t v_off[Geo<D>::VU];    // V row 2*(u&31), chunk u>>5
+  int v_row[Geo<D>::VU];
+};
+
+template <int D>
+__device__ __forceinline__ LoadPlan<D> make_load_plan(int64_t k_st, int64_t v_st, int wave,
+                                                      int lane, int tid) {
+  using G = Geo<D>;
+  LoadPlan<D> p;
+#pragma unroll
+  for (int i = 0; i < G::KDMA; ++i) {
+    const int slot = (i * kWaves + wave) * 64 + lane;
+    const int row = slot / G::CPR;
+    const int chunk = (slot % G::CPR) ^ (row % G::CPR);
+    p.k_row[i] = row;
+    p.k_off[i] = (uint32_t)(row * k_st * 2 + chunk * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < G::VU; ++i) {
+    const int u = tid + i * G::NTH;
+    p.v_row[i] = 2 * (u & 31);
+    p.v_off[i] = (uint32_t)(p.v_row[i] * v_st * 2 + (u >> 5) * 16);
+  }
+  return p;
+}
+
 // K tile: global -> LDS without registers (global_load_lds_dwordx4). Each wave
 // instruction writes 64 consecutive 16-byte LDS slots; slot s of row r holds
 // global chunk s ^ (r mod CPR), which makes the 16 lanes of an MFMA operand
-// read (16 rows, one chunk) hit 16 distinct bank groups. Rows outside [0, T)
-// are clamped to a valid row; every score they produce is masked.
+// read (16 rows, one chunk) hit 16 distinct bank groups. In edge tiles, rows
+// outside [0, T) are clamped to a valid row; every score they produce is masked.
 template <int D, typename T>
 __device__ __forceinline__ void issue_k_tile(T* ks, const T* kp, int64_t k_st, int j0, int T_,
-                                             int wave, int lane) {
+                                             int wave, const LoadPlan<D>& lp, bool interior) {
   using G = Geo<D>;
+  const char* tile = reinterpret_cast<const char*>(kp + (int64_t)j0 * k_st);
 #pragma unroll
   for (int i = 0; i < G::KDMA; ++i) {
+    const char* src;
+    if (interior) {
+      src = tile + lp.k_off[i];
+    } else {
+      int j = j0 + lp.k_row[i];
+      j = j < 0 ? 0 : (j >= T_ ? T_ - 1 : j);
+      src = tile + lp.k_off[i] + (int64_t)(j - j0 - lp.k_row[i]) * k_st * 2;
+    }
     const int base = (i * kWaves + wave) * 64;  // first chunk slot of this instruction
-    const int slot = base + lane;
-    const int row = slot / G::CPR;
-    const int chunk = (slot % G::CPR) ^ (row % G::CPR);
-    int j = j0 + row;
-    j = j < 0 ? 0 : (j >= T_ ? T_ - 1 : j);
-    const T* src = kp + (int64_t)j * k_st + chunk * 8;
     __builtin_amdgcn_global_load_lds(
         (const __attribute__((address_space(1))) void*)src,
         (__attribute__((address_space(3))) void*)(ks + base * 8), 16, 0, 0);
@@ -140,21 +178,26 @@ __device__ __forceinline__ void issue_k_tile(T* ks, const T* kp, int64_t k_st, i
 
 template <int D, typename T>
 __device__ __forceinline__ void load_v_tile(VStage<D>& r, const T* vp, int64_t v_st, int j0,
-                                            int T_, int tid) {
+                                            int T_, const LoadPlan<D>& lp, bool interior) {
   using G = Geo<D>;
+  const char* tile = reinterpret_cast<const char*>(vp + (int64_t)j0 * v_st);
 #pragma unroll
   for (int i = 0; i < G::VU; ++i) {
-    const int u = tid + i * G::NTH;
-    const int ja = j0 + 2 * (u & 31);
-    const int dch = u >> 5;
-    // unconditional loads from clamped rows, zeroed outside [0, T): no branches
-    const int jca = ja < 0 ? 0 : (ja >= T_ ? T_ - 1 : ja);
-    const int jcb = ja + 1 < 0 ? 0 : (ja + 1 >= T_ ? T_ - 1 : ja + 1);
-    const u32x4 a = *reinterpret_cast<const u32x4*>(vp + (int64_t)jca * v_st + dch * 8);
-    const u32x4 b = *reinterpret_cast<const u32x4*>(vp + (int64_t)jcb * v_st + dch * 8);
-    const u32x4 z = {0u, 0u, 0u, 0u};
-    r.va[i] = (ja >= 0 && ja < T_) ? a : z;
-    r.vb[i] = (ja + 1 >= 0 && ja + 1 < T_) ? b : z;
+    if (interior) {
+      r.va[i] = *reinterpret_cast<const u32x4*>(tile + lp.v_off[i]);
+      r.vb[i] = *reinterpret_cast<const u32x4*>(tile + lp.v_off[i] + v_st * 2);
+    } else {
+      // unconditional loads from clamped rows, zeroed outside [0, T): no branches
+      const int ja = j0 + lp.v_row[i];
+      const int jca = ja < 0 ? 0 : (ja >= T_ ? T_ - 1 : ja);
+      const int jcb = ja + 1 < 0 ? 0 : (ja + 1 >= T_ ? T_ - 1 : ja + 1);
+      const char* row0 = tile + lp.v_off[i] - (int64_t)lp.v_row[i] * v_st * 2;
+      const u32x4 a = *reinterpret_cast<const u32x4*>(row0 + (int64_t)(jca - j0) * v_st * 2);
+      const u32x4 b = *reinterpret_cast<const u32x4*>(row0 + (int64_t)(jcb - j0) * v_st * 2);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      r.va[i] = (ja >= 0 && ja < T_) ? a : z;
+      r.vb[i] = (ja + 1 >= 0 && ja + 1 < T_) ? b : z;
+    }
   }
 }
 
@@ -171,8 +214,9 @@ __device__ __forceinline__ void store_v_tile(const VStage<D>& r, T* vt, int tid)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint32_t a = r.va[i][e], b = r.vb[i][e];
-      const uint32_t lo = (a & 0xffffu) | (b << 16);      // d = 8*dch + 2e
-      const uint32_t hi = (a >> 16) | (b & 0xffff0000u);  // d = 8*dch + 2e + 1
+      // v_perm_b32 byte selects over {b:a}: low halves (d = 8*dch + 2e), high halves (+1)
+      const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);
+      const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);
       *reinterpret_cast<uint32_t*>(base + (2 * e) * G::VSTR) = lo;
       *reinterpret_cast<uint32_t*>(base + (2 * e + 1) * G::VSTR) = hi;
     }
@@ -245,7 +289,9 @@ __device__ __forceinline__ void softmax_pv(f32x16 (&s)[2], f32x16 (&o)[Geo<D>::D
   using G = Geo<D>;
   using v8 = typename VecT<T>::v8;
   const int half = lane >> 5;
-  if (need_mask) {
+  // need_mask is wave-uniform; readfirstlane makes that visible to the compiler so
+  // this stays a scalar branch instead of being if-converted onto every tile.
+  if (__builtin_expect(__builtin_amdgcn_readfirstlane((int)need_mask), 0)) {
     const int jb = j0 + 4 * half;
     const unsigned width = (unsigned)(band.hi - band.lo);
 #pragma unroll
@@ -267,7 +313,7 @@ __device__ __forceinline__ void softmax_pv(f32x16 (&s)[2], f32x16 (&o)[Geo<D>::D
   const float m_new = fmaxf(m, mx);
   // m = -inf and a finite m_new give +inf (rescale); both -inf give NaN (no rescale)
   const bool grow = (m_new - m) * c > kRescaleLog2;
-  if (__any(grow)) {
+  if (__builtin_expect(__any(grow), 0)) {
     const float mc_new = (m_new == -INFINITY) ? 0.f : m_new * c;
     const float alpha = fast_exp2(fmaf(m, c, -mc_new));
     l *= alpha;
@@ -277,6 +323,28 @@ __device__ __forceinline__ void softmax_pv(f32x16 (&s)[2], f32x16 (&o)[Geo<D>::D
   }
   const float mc = (m == -INFINITY) ? 0.f : m * c;
   float psum = 0.f;
+  const T* base = vt + (lane & 31) * G::VSTR + half * 8;
+#if TTCD_INTERLEAVE_PV
+  // Softmax and PV interleaved per 16-key MFMA step: only one P^T fragment and
+  // one step's V^T fragments are live, and the exp2 of step ks+1 can overlap
+  // the MFMAs of step ks.
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    v8 pf;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = fast_exp2(fmaf(s[ks >> 1][(ks & 1) * 8 + e], c, -mc));
+      psum += p;
+      pf[e] = static_cast<T>(p);
+    }
+    v8 b[G::DT];
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt)
+      b[dt] = *reinterpret_cast<const v8*>(base + dt * 32 * G::VSTR + ks * 16);
+#pragma unroll
+    for (int dt = 0; dt < G::DT; ++dt) o[dt] = mfma32(b[dt], pf, o[dt]);
+  }
+#else
   v8 pf[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
@@ -287,9 +355,7 @@ __device__ __forceinline__ void softmax_pv(f32x16 (&s)[2], f32x16 (&o)[Geo<D>::D
       pf[ks][e] = static_cast<T>(p);
     }
   }
-  l += psum;
   constexpr int N = 4 * G::DT;
-  const T* base = vt + (lane & 31) * G::VSTR + half * 8;
   v8 b[N];
 #pragma unroll
   for (int i = 0; i < N; ++i)
@@ -297,6 +363,8 @@ __device__ __forceinline__ void softmax_pv(f32x16 (&s)[2], f32x16 (&o)[Geo<D>::D
 #pragma unroll
   for (int i = 0; i < N; ++i) o[i >> 2] = mfma32(b[i], pf[i & 3], o[i >> 2]);
   pipeline_reads_with_mfma<N>();
+#endif
+  l += psum;
 }
 
 // Normalise and store one output (and its LSE) from the O^T accumulator.
@@ -387,11 +455,13 @@ void attn_fwd_kernel(AttnArgs a) {
     n_lo = 1;
   }
 
+  const LoadPlan<D> lp = make_load_plan<D>(a.k_st, a.v_st, wave, lane, tid);
   VStage<D> vr;
   if (n_hi >= n_lo) {
     const int j0 = sc.tile_start(n_hi);
-    issue_k_tile<D, T>(smem, kp, a.k_st, j0, T_, wave, lane);
-    load_v_tile<D, T>(vr, vp, a.v_st, j0, T_, tid);
+    const bool interior = j0 >= 0 && j0 + kBlockN <= T_;
+    issue_k_tile<D, T>(smem, kp, a.k_st, j0, T_, wave, lp, interior);
+    load_v_tile<D, T>(vr, vp, a.v_st, j0, T_, lp, interior);
     store_v_tile<D, T>(vr, smem + G::K_ELEMS, tid);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -404,8 +474,9 @@ void attn_fwd_kernel(AttnArgs a) {
     const bool has_next = n - 1 >= n_lo;
     if (has_next) {
       const int jn = sc.tile_start(n - 1);
-      issue_k_tile<D, T>(nks, kp, a.k_st, jn, T_, wave, lane);
-      load_v_tile<D, T>(vr, vp, a.v_st, jn, T_, tid);
+      const bool interior = jn >= 0 && jn + kBlockN <= T_;
+      issue_k_tile<D, T>(nks, kp, a.k_st, jn, T_, wave, lp, interior);
+      load_v_tile<D, T>(vr, vp, a.v_st, jn, T_, lp, interior);
     }
 
     const int j0 = sc.tile_start(n);
