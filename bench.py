@@ -75,7 +75,7 @@ def cpu_baseline(q, k, v, cfg, target_s: float) -> dict:
     torch.set_num_threads(threads)
     B, T, H, D, wt, ws = cfg["B"], cfg["T"], cfg["Hq"], cfg["D"], cfg["wt"], cfg["ws"]
     r0 = T // 2
-    span = 2048
+    span = 8192
     qc = q[:, r0:r0 + span].cpu()
     kc = k[:, r0 - wt + 1:r0 + span].cpu()
     vc = v[:, r0 - wt + 1:r0 + span].cpu()
@@ -192,7 +192,7 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="qwen3", choices=sorted(CONFIGS))
     ap.add_argument("--no-extra", action="store_true", help="skip comparators and conv")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")

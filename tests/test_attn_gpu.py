@@ -134,8 +134,9 @@ def test_non_aligned_equal_windows(gpu):
     _assert_close(ot, _oracle(q, k, v, 257), torch.bfloat16, "teacher")
 
 
-@pytest.mark.parametrize("wt,ws", [(4128, 4096), (4160, 4096), (4224, 4096), (1216, 1024),
-                                   (8192, 4096), (8192, 7168), (8192, 8064)])
+@pytest.mark.parametrize("wt,ws", [(4097, 4096), (4101, 4096), (4128, 4096), (4160, 4096),
+                                   (4224, 4096), (1216, 1024), (1000, 999), (8192, 4096),
+                                   (8192, 7168), (8192, 8064)])
 @torch.inference_mode()
 def test_narrow_gaps(gpu, wt, ws):
     """test/test_fused_attn_narrow_gap.py:39-51 shape (T=8192, H=8, HK=4, D=128) plus the
