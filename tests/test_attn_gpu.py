@@ -146,9 +146,13 @@ def test_narrow_gaps(gpu, wt, ws):
     q, k, v = make_qkv(batch=1, seqlen=8192, heads=8, kv_heads=4, head_dim=128, seed=0)
     ot, os_ = fused_dual_window_attn(q, k, v, wt, ws)
     rt, rs = window_attn(q, k, v, wt), window_attn(q, k, v, ws)
-    for a, r in ((ot, rt), (os_, rs)):
+    # The single-window kernel tiles keys at offset 0, the dual kernel at
+    # w_S mod 32: different fp32 accumulation order, so up to ~1 bf16 ulp apart.
+    for name, a, r in (("teacher", ot, rt), ("student", os_, rs)):
         d = (a.float() - r.float()).abs()
-        assert d.max().item() < 5e-3 and a.isfinite().all()
+        bound = 4e-3 + 8e-3 * r.float().abs()
+        assert a.isfinite().all() and (d <= bound).all(), (
+            f"{name}: max |diff| {d.max().item():.3g} vs window_attn (bound {bound.max().item():.3g})")
     rows = torch.cat([torch.arange(ws - 40, ws + 100), torch.arange(wt - 64, wt + 64),
                       torch.arange(8192 - 128, 8192)]).clamp(0, 8191).unique()
     for W, out in ((wt, ot), (ws, os_)):

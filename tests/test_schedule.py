@@ -13,10 +13,10 @@ import pytest
 from ttcd_amd import _lib
 
 
-def _coverage(T, dual, a, b):
+def _coverage(T, dual, a, b, group=2):
     near = np.zeros((T, T), dtype=np.int32)
     far = np.zeros((T, T), dtype=np.int32)
-    st = _lib.lib().ttcd_attn_schedule_coverage(T, int(dual), a, b, near.ctypes.data,
+    st = _lib.lib().ttcd_attn_schedule_coverage(T, int(dual), a, b, group, near.ctypes.data,
                                                 far.ctypes.data)
     if st != 0:
         raise AssertionError(_lib.lib().ttcd_last_error().decode())
@@ -38,9 +38,10 @@ DUAL_CASES = [
 ]
 
 
+@pytest.mark.parametrize("group", [2, 3])
 @pytest.mark.parametrize("T,wt,ws", DUAL_CASES)
-def test_dual_schedule_covers_each_pair_once(T, wt, ws):
-    near, far = _coverage(T, True, ws, wt)
+def test_dual_schedule_covers_each_pair_once(T, wt, ws, group):
+    near, far = _coverage(T, True, ws, wt, group)
     WT = T if wt < 0 else wt
     np.testing.assert_array_equal(near, _band(T, 0, ws))
     np.testing.assert_array_equal(near + far, _band(T, 0, WT))
@@ -53,7 +54,7 @@ def test_dual_schedule_narrow_gaps_subsampled(wt, ws):
     # The reference's narrow-gap windows (and BASELINE's 7168/8064 gaps) at a T long
     # enough for every tile/boundary pattern to occur.
     T = 8192 + 384
-    near, far = _coverage(T, True, ws, wt)
+    near, far = _coverage(T, True, ws, wt, 1 + (wt % 2))
     np.testing.assert_array_equal(near, _band(T, 0, ws))
     np.testing.assert_array_equal(far, _band(T, ws, wt))
 
@@ -61,7 +62,8 @@ def test_dual_schedule_narrow_gaps_subsampled(wt, ws):
 @pytest.mark.parametrize("T,lo,hi", [(257, 0, 192), (769, 0, 512), (769, 256, 512),
                                      (500, 499, 10**6), (300, 0, 1), (300, 7, 8),
                                      (129, 128, 129), (64, 100, 200), (1000, 97, 233)])
-def test_band_schedule_covers_each_pair_once(T, lo, hi):
-    near, far = _coverage(T, False, lo, hi)
+@pytest.mark.parametrize("group", [1, 2])
+def test_band_schedule_covers_each_pair_once(T, lo, hi, group):
+    near, far = _coverage(T, False, lo, hi, group)
     np.testing.assert_array_equal(near, _band(T, lo, hi))
     assert not far.any()

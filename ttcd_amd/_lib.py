@@ -62,7 +62,7 @@ _SIGS = {
     "ttcd_causal_dwconv_chunked_fwd": (_i32, [
         _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp]),
     "ttcd_attn_schedule_coverage": (_i32, [
-        _i32, _i32, _i32, _i32, _vp, _vp]),
+        _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
 }
 
 _lock = threading.Lock()

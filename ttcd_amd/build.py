@@ -25,6 +25,9 @@ LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libttcd_amd.so")
 
 SOURCES = ["attn.hip", "conv.hip", "merge.hip", "api.hip"]
+# attn.hip has no NaN-dependent logic; without IEEE mode max/min of MFMA
+# results need no canonicalising moves.
+SOURCE_FLAGS = {"attn.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32.
@@ -73,8 +76,8 @@ def build(verbose: bool = False, jobs: int | None = None, out: str | None = None
     for src in SOURCES:
         obj = os.path.join(build_dir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, *[f"-D{d}" for d in defines], "-I", INCLUDE, "-I",
-                     CSRC, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), *[f"-D{d}" for d in defines],
+                     "-I", INCLUDE, "-I", CSRC, "-c", os.path.join(CSRC, src), "-o", obj])
     jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 4) // 2))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))

@@ -62,7 +62,7 @@ ttcd_status check_attn(const void* q, const void* k, const void* v, const void* 
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return fail(TTCD_ERR_UNSUPPORTED, "tensor base pointers must be 16-byte aligned");
   const int64_t nqb = (T + ttcd::kBlockM - 1) / ttcd::kBlockM;
-  if ((int64_t)B * Hq * nqb > 0x7fffffffLL)
+  if ((int64_t)B * Hq * nqb > 0x7fffffffLL)  // bound on workgroups for either geometry
     return fail(TTCD_ERR_UNSUPPORTED, "grid too large");
   return TTCD_OK;
 }
@@ -91,7 +91,8 @@ ttcd::AttnArgs fill_args(const void* q, const void* k, const void* v, int B, int
   a.Hq = Hq;
   a.Hkv = Hkv;
   a.G = Hq / Hkv;
-  a.nqb = (T + ttcd::kBlockM - 1) / ttcd::kBlockM;
+  const int span = ttcd::wg_span_tokens(a.G);
+  a.nqb = (T + span - 1) / span;  // query blocks per (b, slice)
   a.c = sm_scale * 1.4426950408889634f;
   return a;
 }
@@ -209,9 +210,10 @@ ttcd_status ttcd_causal_dwconv_chunked_fwd(const void* x, const void* w, void* y
 }
 
 ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int window_t,
-                                        int32_t* counts_near, int32_t* counts_far) {
+                                        int gqa_group, int32_t* counts_near,
+                                        int32_t* counts_far) {
   using namespace ttcd;
-  if (T < 1 || !counts_near || (dual && !counts_far))
+  if (T < 1 || gqa_group < 1 || !counts_near || (dual && !counts_far))
     return fail(TTCD_ERR_INVALID_ARGUMENT, "bad coverage arguments");
   Schedule sc;
   if (dual) {
@@ -224,44 +226,61 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
       return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi");
     sc = make_band_schedule(T, window_s, window_t);
   }
-  const int nqb = (T + kBlockM - 1) / kBlockM;
-  for (int qb = 0; qb < nqb; ++qb) {
-    const int t0 = qb * kBlockM;
-    const int t_last = (t0 + kBlockM < T ? t0 + kBlockM : T) - 1;
+  // Workgroup geometry as launched (attn.hip): both groups over the same 128
+  // tokens (two heads) for an even GQA group, else the two groups over the
+  // halves of 256 tokens of one head. The slice's rows are owned by the waves
+  // r0 = t0 + 32*w for w < span/32; the slot plan is built from all 8 waves.
+  const bool paired = gqa_group % 2 == 0;
+  const int span = wg_span_tokens(gqa_group);
+  const int nwg = (T + span - 1) / span;
+  for (int qb = 0; qb < nwg; ++qb) {
+    const int t0 = qb * span;
+    const int t_last = (t0 + span < T ? t0 + span : T) - 1;
     int n_hi, n_lo;
     if (!sc.wg_range(t0, t_last, &n_hi, &n_lo)) continue;
-    for (int w = 0; w < kWaves; ++w) {
+    auto r0_of_wave = [&](int wv) {
+      return t0 + (paired ? 0 : (wv / kGroupWaves) * kBlockM) + (wv % kGroupWaves) * kWaveRows;
+    };
+    const SlotPlan sp = make_slot_plan(sc, r0_of_wave, n_hi, n_lo);
+    if (sp.ndup > kWalkDup)
+      return fail(TTCD_ERR_UNSUPPORTED, "schedule error: %d repeated tiles > %d", sp.ndup, kWalkDup);
+    for (int w = 0; w < span / kWaveRows; ++w) {
       const int r0 = t0 + w * kWaveRows;
       if (r0 >= T) continue;
-      bool done1 = false;  // phase 1 finished (student output emitted)
-      for (int n = n_hi; n >= n_lo; --n) {
+      bool student_done = false;
+      SlotWalker walk(sp);  // the kernel's incremental form of the plan
+      for (int k = 0; k < sp.slots(); ++k, walk.advance()) {
+        bool repeat;
+        const int n = sp.tile(k, &repeat);
+        if (walk.n != n || walk.rep != repeat)
+          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: walker (%d,%d) != plan (%d,%d) at slot %d",
+                      walk.n, (int)walk.rep, n, (int)repeat, k);
         const int j0 = sc.tile_start(n);
-        const bool in1 = wave_touches(r0, sc.p1, j0);
-        const bool in2 = sc.dual && wave_touches(r0, sc.p2, j0);
-        for (int phase = 1; phase <= 2; ++phase) {
-          const bool in = phase == 1 ? in1 : in2;
-          if (!in) continue;
-          const Band band = phase == 1 ? sc.p1 : sc.p2;
-          if (phase == 1 && done1)
-            return fail(TTCD_ERR_UNSUPPORTED, "schedule error: phase-1 tile after emit (r0=%d n=%d)",
-                        r0, n);
-          if (phase == 2 && !done1 && !(in1 && wave_last(r0, sc.p1, j0)))
-            return fail(TTCD_ERR_UNSUPPORTED,
-                        "schedule error: phase-2 tile before student emit (r0=%d n=%d)", r0, n);
-          const bool full = wave_full(r0, band, j0);
-          for (int i = r0; i < r0 + kWaveRows && i < T; ++i) {
-            for (int j = j0; j < j0 + kBlockN; ++j) {
-              const bool inc = full || visible(i, j, band, T);
-              if (!inc) continue;
-              if (j < 0 || j >= T)
-                return fail(TTCD_ERR_UNSUPPORTED, "schedule error: key %d out of range", j);
-              int32_t* cnt = phase == 1 ? counts_near : counts_far;
-              cnt[(int64_t)i * T + j] += 1;
-            }
+        const int act = slot_action(sc, r0, j0, repeat);
+        if (act == kSkip) continue;
+        const bool far = act == kBand2 || act == kFar;
+        if (sc.dual && !far && student_done)
+          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: student keys after emit (r0=%d k=%d)",
+                      r0, k);
+        if (sc.dual && far && !student_done)
+          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: far keys before emit (r0=%d k=%d)",
+                      r0, k);
+        const Band band = far ? sc.p2 : sc.p1;
+        const bool full = wave_full(r0, band, j0);
+        for (int i = r0; i < r0 + kWaveRows && i < T; ++i) {
+          for (int j = j0; j < j0 + kBlockN; ++j) {
+            if (!(full || visible(i, j, band, T))) continue;
+            if (j < 0 || j >= T)
+              return fail(TTCD_ERR_UNSUPPORTED, "schedule error: key %d out of range", j);
+            int32_t* cnt = far ? counts_far : counts_near;
+            cnt[(int64_t)i * T + j] += 1;
           }
-          if (phase == 1 && wave_last(r0, sc.p1, j0)) done1 = true;
         }
+        if (act == kStudentLast) student_done = true;
       }
+      if (sc.dual && !student_done && sc.p1.lo < sc.p1.hi)
+        return fail(TTCD_ERR_UNSUPPORTED, "schedule error: student output never written (r0=%d)",
+                    r0);
     }
   }
   return ok();

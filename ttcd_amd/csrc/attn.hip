@@ -6,32 +6,44 @@
 // calls of the LSE variant (profiling/lse_dual_attn.py:22-29, :143-149).
 //
 // Mapping onto CDNA4
-//   * One workgroup = 4 wavefronts = 128 query tokens of one query head; the
-//     K/V tile (64 keys) is staged once in LDS and read by all 4 waves.
+//   * One workgroup = 8 wavefronts (two groups of 4) sharing each K/V tile:
+//     two query heads of one K/V head over 128 tokens when the GQA group is
+//     even, else one head over 256 tokens. Each wavefront owns 32 query rows.
+//     One workgroup per CU (2 wavefronts per SIMD).
+//   * K and V tiles (64 keys) go global -> LDS by DMA
+//     (global_load_lds_dwordx4, no registers), 4 stages deep (each tile is
+//     fetched three slots before its V part is read). Rows are
+//     stored with their 16-byte chunks XOR-swizzled so every operand read
+//     below is free of bank conflicts.
 //   * Scores are produced TRANSPOSED, S^T = K Q^T, with
-//     v_mfma_f32_32x32x16_{bf16,f16}: in the 32x32 accumulator layout every
-//     lane owns one query (column lane%32) and 16 of the 32 keys (rows), the
-//     other 16 living in lane^32. Row max / row sum are therefore in-register
-//     reductions plus one cross-half exchange, and the online-softmax rescale
-//     factor is a per-lane scalar.
-//   * O^T = V^T P^T accumulates in 4 (D=128) or 2 (D=64) 32x32 fp32 tiles.
-//     P^T is consumed straight from the score registers (bf16/f16-rounded);
-//     the MFMA k-slot <-> key assignment this implies (bits 2 and 3 of the
-//     key index swapped inside each 16-key step) is absorbed by the LDS
-//     layout of V^T, which the staging code writes transposed.
-//   * LDS tiles are padded (K rows D+8, V^T rows 64+8 elements) so the
-//     16-byte operand reads of 16 consecutive lanes hit distinct banks.
-//   * K/V tiles are double-buffered: the global loads of tile n-1 are issued
-//     before the MFMA work on tile n and written to LDS after it; one
-//     workgroup barrier per tile.
+//     v_mfma_f32_32x32x16_{bf16,f16}: each lane owns one query (column
+//     lane%32) and 16 of the 32 keys (rows); the other 16 live in lane^32.
+//     Row max / row sum are in-register reductions plus one
+//     v_permlane32_swap, and the online-softmax rescale factor is a
+//     per-lane scalar.
+//   * O^T = V^T P^T accumulates in D/32 32x32 fp32 tiles. P^T comes straight
+//     from the score registers (exp2, then rounded to bf16/f16); V^T operands
+//     are read from the row-major V tile with ds_read_b64_tr_b16, which
+//     transposes 4x4 blocks of 16-bit elements across lanes. The key order
+//     of the P^T k-slots (bits 2 and 3 of the key index swapped inside each
+//     16-key step) is matched by the rows each transposed read selects.
+//   * Software pipeline inside each wavefront: while the MFMAs of the next
+//     slot's scores S(k+1) run, the VALU computes exp2 of S(k); the PV MFMAs
+//     of slot k then run while the VALU reduces the row max of S(k+1).
 //   * Workgroups are remapped so each XCD (own L2) sweeps a contiguous run of
-//     (b, kv-head, q-tile, q-head-in-group), i.e. the GQA heads sharing a K/V
-//     head and neighbouring query tiles share that XCD's L2.
+//     (b, kv head, query block, slice); heaviest query blocks first.
 //
 // Numerics follow the reference kernel (fused_dual_attn.py:1-13, :100-107):
 // raw-domain running max, p = exp2(s*c - m*c) with c = sm_scale*log2(e),
 // the m == -inf -> 0 guard, P rounded to the input dtype before PV, l summed
 // from the unrounded fp32 p, epilogue acc * (1/l) rounded to nearest-even.
+// The running max used in exp2 moves only when a row's max grows by more than
+// 2^8 (lazy rescale; softmax is invariant to it up to rounding).
+//
+// Built with -fno-honor-nans -mno-amdgpu-ieee (ttcd_amd/build.py): no value
+// here is NaN for finite inputs (masked scores are -inf, every test below is
+// written without relying on NaN comparisons), and IEEE mode would make each
+// fmaxf of an MFMA result re-canonicalise its inputs first.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -39,23 +51,17 @@
 #include "internal.h"
 #include "schedule.h"
 
-#ifndef TTCD_WAVES_PER_EU
-#define TTCD_WAVES_PER_EU 2
-#endif
-#ifndef TTCD_INTERLEAVE_PV
-#define TTCD_INTERLEAVE_PV 1
-#endif
-
 namespace ttcd {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define LDS_AS __attribute__((address_space(3)))
+#define GLB_AS __attribute__((address_space(1)))
 
 template <typename T>
 struct VecT;
@@ -63,11 +69,18 @@ template <>
 struct VecT<__bf16> {
   typedef bf16x8 v8;
   typedef bf16x4 v4;
+  __device__ static bf16x4 read_tr(const LDS_AS char* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((LDS_AS bf16x4*)p);
+  }
 };
 template <>
 struct VecT<_Float16> {
   typedef f16x8 v8;
   typedef f16x4 v4;
+  typedef __fp16 h4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+  __device__ static f16x4 read_tr(const LDS_AS char* p) {
+    return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((LDS_AS h4*)p));
+  }
 };
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
@@ -79,8 +92,21 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Workgroup id -> logical tile id such that XCD x (which receives ids
-// g = x, x+8, ...) processes one contiguous range of logical ids.
+// Values of lanes l and l^32 combined: v_permlane32_swap of v with itself
+// leaves the low half's values in one result and the high half's in the other.
+__device__ __forceinline__ float xhalf_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Workgroup id -> logical id such that XCD x (which receives ids g = x, x+8,
+// ...) processes one contiguous range of logical ids.
 __device__ __forceinline__ int xcd_remap(int g, int total) {
   constexpr int kXcd = 8;
   const int q = total / kXcd, r = total % kXcd;
@@ -90,281 +116,156 @@ __device__ __forceinline__ int xcd_remap(int g, int total) {
 
 template <int D>
 struct Geo {
-  static constexpr int CPR = D / 8;          // 16-byte chunks per K row
-  static constexpr int VSTR = kBlockN + 8;   // V^T tile row stride (elements)
-  static constexpr int K_ELEMS = kBlockN * D;  // K tile, rows unpadded, chunks XOR-swizzled
-  static constexpr int V_ELEMS = D * VSTR;
-  static constexpr int STAGE = K_ELEMS + V_ELEMS;
-  static constexpr int DK = D / 16;  // MFMA k-steps of S^T = K Q^T
-  static constexpr int DT = D / 32;  // 32-row d tiles of O^T
+  static constexpr int RB = D * 2;                 // bytes per K / V row
+  static constexpr int CPR = D / 8;                // 16-byte chunks per row
+  static constexpr int TILE_B = kBlockN * RB;      // bytes of one K or V tile
+  static constexpr int STAGE_B = 2 * TILE_B;       // K tile, then V tile
+  static constexpr int NSTAGE = 4;                 // tile k+3 loads while k+1 / k are read
+  static constexpr int DK = D / 16;                // MFMA k-steps of S^T = K Q^T
+  static constexpr int DT = D / 32;                // 32-row d tiles of O^T
   static constexpr int NTH = kWaves * 64;
-  static constexpr int KDMA = kBlockN * CPR / NTH;          // direct K loads per thread
-  static constexpr int VU = (kBlockN / 2) * CPR / NTH;      // (2 keys x 8 d) V units per thread
-  static_assert(KDMA * NTH == kBlockN * CPR, "K tile must split evenly");
-  static_assert(VU * NTH == (kBlockN / 2) * CPR, "V tile must split evenly");
+  static constexpr int NDMA = kBlockN * CPR / NTH;  // 16-byte DMA loads per lane per tile
+  static_assert(NDMA >= 1 && NDMA * NTH == kBlockN * CPR, "tile must split evenly");
 };
 
+// LDS chunk swizzles (16-byte chunk c of row r is stored at chunk c ^ swz(r)).
+// K: the 16 lanes of one ds_read_b128 pass read 16 consecutive rows at one
+// chunk -> 16 distinct bank groups. V: the 32 lanes of one ds_read_b64_tr_b16
+// pass read 4 consecutive rows x 4 consecutive chunks -> 16 distinct groups.
 template <int D>
-struct VStage {
-  u32x4 va[Geo<D>::VU];
-  u32x4 vb[Geo<D>::VU];
-};
-
-// Position of key kk (0..63 inside the tile) in a V^T row: bits 2 and 3
-// swapped, matching the key held by MFMA k-slot (lane/32)*8 + e of the P^T
-// operand built from the S^T accumulator registers.
-__device__ __forceinline__ int vt_pos(int kk) {
-  return (kk & ~15) | (kk & 3) | ((kk >> 3) & 1) << 2 | ((kk >> 2) & 1) << 3;
+__device__ __forceinline__ int swz_k(int r) {
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int r) {
+  return D == 128 ? ((r & 3) << 2) : (((r >> 1) & 1) << 2);
 }
 
-// Per-thread byte offsets of this thread's tile loads relative to the tile's
-// first key row; computed once, so a tile costs one scalar base update.
+// Per-lane constants: DMA source offsets and LDS operand addresses.
 template <int D>
-struct LoadPlan {
-  uint32_t k_off[Geo<D>::KDMA];  // K chunk this lane moves per direct load
-  int k_row[Geo<D>::KDMA];
-  uint32_t v_off[Geo<D>::VU];    // V row 2*(u&31), chunk u>>5
-  int v_row[Geo<D>::VU];
+struct Lane {
+  uint32_t k_off[Geo<D>::NDMA];  // byte offset of this lane's K chunk in an interior tile
+  uint32_t v_off[Geo<D>::NDMA];
+  uint32_t xk;                   // K operand address inside a tile (XOR ks << 5 per k-step)
+  uint32_t vb[Geo<D>::DT];       // V^T operand address inside a tile per d tile
 };
 
+// DMA slot geometry: the lane's i-th load of a tile writes 16-byte LDS slot
+// (wave + 8i)*64 + lane, i.e. tile row `row`, physical chunk `pch`.
 template <int D>
-__device__ __forceinline__ LoadPlan<D> make_load_plan(int64_t k_st, int64_t v_st, int wave,
-                                                      int lane, int tid) {
+__device__ __forceinline__ void dma_slot_of(int wave, int lane, int i, int* row, int* pch) {
+  const int slot = (wave + kWaves * i) * 64 + lane;
+  *row = slot / Geo<D>::CPR;
+  *pch = slot % Geo<D>::CPR;
+}
+
+template <int D>
+__device__ __forceinline__ Lane<D> make_lane(int64_t k_st, int64_t v_st, int wave, int lane) {
   using G = Geo<D>;
-  LoadPlan<D> p;
+  Lane<D> p;
 #pragma unroll
-  for (int i = 0; i < G::KDMA; ++i) {
-    const int slot = (i * kWaves + wave) * 64 + lane;
-    const int row = slot / G::CPR;
-    const int chunk = (slot % G::CPR) ^ (row % G::CPR);
-    p.k_row[i] = row;
-    p.k_off[i] = (uint32_t)(row * k_st * 2 + chunk * 16);
+  for (int i = 0; i < G::NDMA; ++i) {
+    int row, pch;
+    dma_slot_of<D>(wave, lane, i, &row, &pch);
+    p.k_off[i] = (uint32_t)(row * k_st * 2) + (uint32_t)((pch ^ swz_k<D>(row)) * 16);
+    p.v_off[i] = (uint32_t)(row * v_st * 2) + (uint32_t)((pch ^ swz_v<D>(row)) * 16);
   }
+  {
+    // S^T A operand: lane reads row r = lane%32 (+32 per key block), logical
+    // chunk 2*ks + h; physical chunk (2ks + h) ^ s = ((s & ~1) ^ 2ks) | ((h ^ s) & 1).
+    const int r = lane & 31, h = lane >> 5, s = swz_k<D>(r);
+    p.xk = (uint32_t)(r * G::RB + (((h ^ s) & 1) << 4) + ((s & ~1) << 4));
+  }
+  {
+    // O^T A operand from ds_read_b64_tr_b16: lane i of 16-lane group g names
+    // key kb + (i >> 2), d = 32*dt + 16*(g & 1) + 4*(i & 3); lane i then
+    // receives keys kb..kb+3 at d = 32*dt + 16*(g & 1) + i.
+    const int i = lane & 15, g = lane >> 4;
+    const int h = g >> 1, q = i >> 2;
+    const int c_lo = 2 * (g & 1) + ((i & 3) >> 1);
 #pragma unroll
-  for (int i = 0; i < G::VU; ++i) {
-    const int u = tid + i * G::NTH;
-    p.v_row[i] = 2 * (u & 31);
-    p.v_off[i] = (uint32_t)(p.v_row[i] * v_st * 2 + (u >> 5) * 16);
+    for (int dt = 0; dt < G::DT; ++dt)
+      p.vb[dt] = (uint32_t)((4 * h + q) * G::RB + (((4 * dt + c_lo) ^ swz_v<D>(q)) << 4) +
+                            (i & 1) * 8);
   }
   return p;
 }
 
-// K tile: global -> LDS without registers (global_load_lds_dwordx4). Each wave
-// instruction writes 64 consecutive 16-byte LDS slots; slot s of row r holds
-// global chunk s ^ (r mod CPR), which makes the 16 lanes of an MFMA operand
-// read (16 rows, one chunk) hit 16 distinct bank groups. In edge tiles, rows
-// outside [0, T) are clamped to a valid row; every score they produce is masked.
-template <int D, typename T>
-__device__ __forceinline__ void issue_k_tile(T* ks, const T* kp, int64_t k_st, int j0, int T_,
-                                             int wave, const LoadPlan<D>& lp, bool interior) {
+// One 16-byte-per-lane DMA: 64 lanes x 16 bytes from base + voff (per lane)
+// into LDS bytes [lds_addr, lds_addr + 1024). Written as inline asm so the
+// compiler does not treat every later LDS read as possibly aliasing the DMA
+// (which makes it wait for the whole load queue); ordering against LDS reads
+// is explicit: s_waitcnt vmcnt + s_barrier in the slot loop.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds_addr) {
+  // base and lds_addr are wave-uniform; readfirstlane makes that explicit.
+  // (It returns int: widen through uint32_t so the low word is not sign-extended.)
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint64_t bs = (uint64_t)lo | ((uint64_t)hi << 32);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
+               :
+               : "v"(voff), "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "s"(bs)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Issue the DMA of one K or V tile (rows j0 .. j0+63) into LDS at byte
+// address `dst`. Rows outside [0, T) are clamped to valid rows; every score
+// they produce is masked and every probability they meet is exactly 0.
+template <int D, typename T, bool IS_K>
+__device__ __forceinline__ void dma_tile(uint32_t dst, const T* base, int64_t st, int j0, int T_,
+                                         int wave, int lane, const uint32_t (&off)[Geo<D>::NDMA],
+                                         bool interior) {
   using G = Geo<D>;
-  const char* tile = reinterpret_cast<const char*>(kp + (int64_t)j0 * k_st);
+  const T* tile = base + (int64_t)j0 * st;
 #pragma unroll
-  for (int i = 0; i < G::KDMA; ++i) {
-    const char* src;
-    if (interior) {
-      src = tile + lp.k_off[i];
-    } else {
-      int j = j0 + lp.k_row[i];
+  for (int i = 0; i < G::NDMA; ++i) {
+    uint32_t voff = off[i];
+    if (!interior) {
+      int row, pch;
+      dma_slot_of<D>(wave, lane, i, &row, &pch);
+      int j = j0 + row;
       j = j < 0 ? 0 : (j >= T_ ? T_ - 1 : j);
-      src = tile + lp.k_off[i] + (int64_t)(j - j0 - lp.k_row[i]) * k_st * 2;
+      const int sw = IS_K ? swz_k<D>(row) : swz_v<D>(row);
+      voff = (uint32_t)((j - j0) * st * 2) + (uint32_t)((pch ^ sw) * 16);
     }
-    const int base = (i * kWaves + wave) * 64;  // first chunk slot of this instruction
-    __builtin_amdgcn_global_load_lds(
-        (const __attribute__((address_space(1))) void*)src,
-        (__attribute__((address_space(3))) void*)(ks + base * 8), 16, 0, 0);
+    dma16(tile, voff, dst + (wave + kWaves * i) * 1024);
   }
 }
 
-template <int D, typename T>
-__device__ __forceinline__ void load_v_tile(VStage<D>& r, const T* vp, int64_t v_st, int j0,
-                                            int T_, const LoadPlan<D>& lp, bool interior) {
-  using G = Geo<D>;
-  const char* tile = reinterpret_cast<const char*>(vp + (int64_t)j0 * v_st);
-#pragma unroll
-  for (int i = 0; i < G::VU; ++i) {
-    if (interior) {
-      r.va[i] = *reinterpret_cast<const u32x4*>(tile + lp.v_off[i]);
-      r.vb[i] = *reinterpret_cast<const u32x4*>(tile + lp.v_off[i] + v_st * 2);
-    } else {
-      // unconditional loads from clamped rows, zeroed outside [0, T): no branches
-      const int ja = j0 + lp.v_row[i];
-      const int jca = ja < 0 ? 0 : (ja >= T_ ? T_ - 1 : ja);
-      const int jcb = ja + 1 < 0 ? 0 : (ja + 1 >= T_ ? T_ - 1 : ja + 1);
-      const char* row0 = tile + lp.v_off[i] - (int64_t)lp.v_row[i] * v_st * 2;
-      const u32x4 a = *reinterpret_cast<const u32x4*>(row0 + (int64_t)(jca - j0) * v_st * 2);
-      const u32x4 b = *reinterpret_cast<const u32x4*>(row0 + (int64_t)(jcb - j0) * v_st * 2);
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      r.va[i] = (ja >= 0 && ja < T_) ? a : z;
-      r.vb[i] = (ja + 1 >= 0 && ja + 1 < T_) ? b : z;
-    }
-  }
-}
-
-// V tile registers -> LDS transposed (V^T rows = d, key positions vt_pos).
-template <int D, typename T>
-__device__ __forceinline__ void store_v_tile(const VStage<D>& r, T* vt, int tid) {
-  using G = Geo<D>;
-#pragma unroll
-  for (int i = 0; i < G::VU; ++i) {
-    const int u = tid + i * G::NTH;
-    const int kk = 2 * (u & 31);
-    const int dch = u >> 5;
-    T* base = vt + (dch * 8) * G::VSTR + vt_pos(kk);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t a = r.va[i][e], b = r.vb[i][e];
-      // v_perm_b32 byte selects over {b:a}: low halves (d = 8*dch + 2e), high halves (+1)
-      const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);
-      const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);
-      *reinterpret_cast<uint32_t*>(base + (2 * e) * G::VSTR) = lo;
-      *reinterpret_cast<uint32_t*>(base + (2 * e + 1) * G::VSTR) = hi;
-    }
-  }
-}
-
-// Scheduling masks of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedDsRead = 0x100;
-
-// Interleave N LDS operand reads with the N MFMAs that consume them, two
-// reads in flight: r r (M r)* M M.
-template <int N>
-__device__ __forceinline__ void pipeline_reads_with_mfma() {
-  __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-#pragma unroll
-  for (int i = 0; i < N - 2; ++i) {
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
-}
-
-// S^T (64 keys x 32 queries) of the current tile: two 32x32 fp32 tiles.
-template <int D, typename T>
-__device__ __forceinline__ void compute_scores(f32x16 (&s)[2], const T* ks,
-                                               const typename VecT<T>::v8 (&qf)[Geo<D>::DK],
-                                               int lane) {
-  using G = Geo<D>;
-  using v8 = typename VecT<T>::v8;
-  constexpr int N = 2 * G::DK;
-  const int r = lane & 31;
-  // Chunk 2*ks + half of row r lives in slot (2*ks) ^ y, y = half ^ (r mod CPR).
-  // Row bases are multiples of the row size, so the byte offset of every
-  // (kt, ks) operand is one XOR of a per-lane base with a constant (plus the
-  // kt row block). The empty asm keeps the compiler from hoisting all DK
-  // XOR results out of the tile loop into DK live registers.
-  uint32_t xbase = (uint32_t)(r * D * 2) | (uint32_t)(((lane >> 5) ^ (r % G::CPR)) << 4);
-  asm volatile("" : "+v"(xbase));
-  const char* kb = reinterpret_cast<const char*>(ks);
-  v8 a[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const uint32_t off = (xbase ^ (uint32_t)((i % G::DK) << 5)) + (i / G::DK) * 32 * D * 2;
-    a[i] = *reinterpret_cast<const v8*>(kb + off);
-  }
-  s[0] = f32x16{};
-  s[1] = f32x16{};
-#pragma unroll
-  for (int i = 0; i < N; ++i) s[i / G::DK] = mfma32(a[i], qf[i % G::DK], s[i / G::DK]);
-  pipeline_reads_with_mfma<N>();
-}
-
-// Lazy online-softmax rescale: the running max used for exp2 is only moved
-// when some row's true max exceeds it by more than 2^kRescaleLog2 (so p stays
-// <= 256 and l, O^T cannot overflow). Softmax is invariant to the reference
-// max, so results are the same up to rounding, and the O^T rescale (a VALU
-// pass over the whole accumulator) leaves the common path: with the
-// diagonal tile first, rows almost never raise their max by 2^8 later.
+// Rescale threshold of the lazy online softmax (log2 units).
 constexpr float kRescaleLog2 = 8.0f;
 
-// One online-softmax step of band {lo, hi} over the tile starting at key j0:
-// masks S in place (if the tile is not entirely inside the band), updates the
-// running max m / per-lane partial sum l, rescales O^T when needed and
-// accumulates P^T through V^T.
-template <int D, typename T>
-__device__ __forceinline__ void softmax_pv(f32x16 (&s)[2], f32x16 (&o)[Geo<D>::DT], float& m,
-                                           float& l, float c, const T* vt, int lane,
-                                           bool need_mask, int qrow, int j0, int T_, Band band) {
-  using G = Geo<D>;
-  using v8 = typename VecT<T>::v8;
-  const int half = lane >> 5;
-  // need_mask is wave-uniform; readfirstlane makes that visible to the compiler so
-  // this stays a scalar branch instead of being if-converted onto every tile.
-  if (__builtin_expect(__builtin_amdgcn_readfirstlane((int)need_mask), 0)) {
-    const int jb = j0 + 4 * half;
-    const unsigned width = (unsigned)(band.hi - band.lo);
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int j = jb + kt * 32 + 8 * (i >> 2) + (i & 3);
-        const bool ok = (unsigned)(qrow - j - band.lo) < width && (unsigned)j < (unsigned)T_;
-        s[kt][i] = ok ? s[kt][i] : -INFINITY;
-      }
-    }
-  }
-  float mx = -INFINITY;
+// Key index of S^T accumulator element e of key block kt for this lane.
+__device__ __forceinline__ int key_of(int j0, int kt, int e, int half) {
+  return j0 + kt * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
+}
+
+// Mask S^T of the tile at j0 to band b (in place).
+__device__ __forceinline__ void mask_band(f32x16 (&s)[2], int qrow, int j0, int T_, Band b,
+                                          int half) {
+  const unsigned width = (unsigned)(b.hi - b.lo);
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float m_new = fmaxf(m, mx);
-  // m = -inf and a finite m_new give +inf (rescale); both -inf give NaN (no rescale)
-  const bool grow = (m_new - m) * c > kRescaleLog2;
-  if (__builtin_expect(__any(grow), 0)) {
-    const float mc_new = (m_new == -INFINITY) ? 0.f : m_new * c;
-    const float alpha = fast_exp2(fmaf(m, c, -mc_new));
-    l *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < G::DT; ++dt) o[dt] *= alpha;
-    m = m_new;
-  }
-  const float mc = (m == -INFINITY) ? 0.f : m * c;
-  float psum = 0.f;
-  const T* base = vt + (lane & 31) * G::VSTR + half * 8;
-#if TTCD_INTERLEAVE_PV
-  // Softmax and PV interleaved per 16-key MFMA step: only one P^T fragment and
-  // one step's V^T fragments are live, and the exp2 of step ks+1 can overlap
-  // the MFMAs of step ks.
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    v8 pf;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p = fast_exp2(fmaf(s[ks >> 1][(ks & 1) * 8 + e], c, -mc));
-      psum += p;
-      pf[e] = static_cast<T>(p);
+    for (int e = 0; e < 16; ++e) {
+      const int j = key_of(j0, kt, e, half);
+      const bool ok = (unsigned)(qrow - j - b.lo) < width && (unsigned)j < (unsigned)T_;
+      s[kt][e] = ok ? s[kt][e] : -INFINITY;
     }
-    v8 b[G::DT];
+}
+
+__device__ __forceinline__ float tile_max(const f32x16 (&s)[2]) {
+  float a = -INFINITY, b = -INFINITY;
 #pragma unroll
-    for (int dt = 0; dt < G::DT; ++dt)
-      b[dt] = *reinterpret_cast<const v8*>(base + dt * 32 * G::VSTR + ks * 16);
-#pragma unroll
-    for (int dt = 0; dt < G::DT; ++dt) o[dt] = mfma32(b[dt], pf, o[dt]);
+  for (int e = 0; e < 16; e += 2) {
+    a = fmaxf(a, fmaxf(s[0][e], s[0][e + 1]));
+    b = fmaxf(b, fmaxf(s[1][e], s[1][e + 1]));
   }
-#else
-  v8 pf[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p = fast_exp2(fmaf(s[ks >> 1][(ks & 1) * 8 + e], c, -mc));
-      psum += p;
-      pf[ks][e] = static_cast<T>(p);
-    }
-  }
-  constexpr int N = 4 * G::DT;
-  v8 b[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i)
-    b[i] = *reinterpret_cast<const v8*>(base + (i >> 2) * 32 * G::VSTR + (i & 3) * 16);
-#pragma unroll
-  for (int i = 0; i < N; ++i) o[i >> 2] = mfma32(b[i], pf[i & 3], o[i >> 2]);
-  pipeline_reads_with_mfma<N>();
-#endif
-  l += psum;
+  return xhalf_max(fmaxf(a, b));
 }
 
 // Normalise and store one output (and its LSE) from the O^T accumulator.
@@ -373,7 +274,7 @@ __device__ __forceinline__ void emit(const f32x16 (&o)[Geo<D>::DT], float m, flo
                                      T* out, int64_t o_st, float* lse, int qrow, int T_,
                                      int lane) {
   using v4 = typename VecT<T>::v4;
-  const float lt = l + __shfl_xor(l, 32);
+  const float lt = xhalf_sum(l);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
   if (qrow >= T_) return;
   const int half = lane >> 5;
@@ -394,125 +295,360 @@ __device__ __forceinline__ void emit(const f32x16 (&o)[Geo<D>::DT], float m, flo
   }
 }
 
+// Everything the slot body needs besides the per-slot registers.
+template <int D, typename T>
+struct Ctx {
+  using v8 = typename VecT<T>::v8;
+  LDS_AS char* lds;
+  v8 qf[Geo<D>::DK];  // Q^T B operands: lane holds query qrow, d = 16*ks + 8*(lane/32) + e
+  Lane<D> ln;
+  float c;
+  int qrow, half, T_;
+};
+
+// K operand i of the scores (key block i & 1, k-step i >> 1).
+template <int D, typename T>
+__device__ __forceinline__ typename VecT<T>::v8 read_k(const LDS_AS char* kb, uint32_t xk, int i) {
+  using v8 = typename VecT<T>::v8;
+  return *(const LDS_AS v8*)(kb + (xk ^ (uint32_t)((i >> 1) << 5)) + (i & 1) * 32 * Geo<D>::RB);
+}
+
+// V^T A operand of 16-key step ks from the lane's transposed-read address vb
+// of one d tile (two reads: keys +0..3 and +8..11 of the step for this lane).
+template <int D, typename T>
+__device__ __forceinline__ typename VecT<T>::v8 read_vt(const LDS_AS char* vb, int ks) {
+  using G = Geo<D>;
+  const auto lo = VecT<T>::read_tr(vb + (16 * ks) * G::RB);
+  const auto hi = VecT<T>::read_tr(vb + (16 * ks + 8) * G::RB);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Score element idx (0..31) of the lane in P^T k-step order: k-step idx / 8,
+// slot idx % 8 -> accumulator element (k-step & 1) * 8 + slot of key block
+// k-step / 2.
+__device__ __forceinline__ float score_at(const f32x16 (&s)[2], int idx) {
+  return s[(idx >> 3) >> 1][((idx >> 3) & 1) * 8 + (idx & 7)];
+}
+__device__ __forceinline__ void score_set(f32x16 (&s)[2], int idx, float v) {
+  s[(idx >> 3) >> 1][((idx >> 3) & 1) * 8 + (idx & 7)] = v;
+}
+
+// One slot of the software pipeline, in issue order (sched_barrier fences
+// keep the compiler from regrouping it):
+//   phase 1: the scores S(k+1) from the K tile at kb (2*DK MFMAs), with the
+//            exp2 / bf16 packing of S(k) spread between them and the K
+//            operand reads R1 MFMAs ahead;
+//   phase 2: PV(k) from the V tile at vbase (4*DT MFMAs), with the row sum of
+//            S(k) and then the row max of S(k+1) spread between them and the
+//            V^T operand reads R2 MFMAs ahead.
+// mc = +inf turns every p of S(k) into exactly 0 (a slot this wave skips).
+// Returns this lane's (unmasked) max of S(k+1), not yet combined across halves.
+template <int D, typename T>
+__device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], f32x16 (&sn)[2],
+                                           f32x16 (&o)[Geo<D>::DT], float& l, float mc,
+                                           const LDS_AS char* kb, const LDS_AS char* vbase) {
+  using G = Geo<D>;
+  using v8 = typename VecT<T>::v8;
+  constexpr int N1 = 2 * G::DK;  // score MFMAs
+  constexpr int N2 = 4 * G::DT;  // PV MFMAs
+  constexpr int R1 = 3;
+  constexpr int R2 = 2;
+  constexpr int E1 = 32 / N1;    // scores exponentiated per score MFMA
+  constexpr int H2 = N2 / 2;     // PV MFMAs carrying sums (the rest carry maxima)
+  constexpr int A2 = 32 / H2;    // values summed / maxed per PV MFMA
+
+  // Lane addresses, opaque per slot so the compiler forms the derived
+  // addresses here instead of holding them all in registers.
+  uint32_t xk = x.ln.xk;
+  asm volatile("" : "+v"(xk));
+  const LDS_AS char* vb[G::DT];
+#pragma unroll
+  for (int dt = 0; dt < G::DT; ++dt) {
+    uint32_t a = x.ln.vb[dt];
+    asm volatile("" : "+v"(a));
+    vb[dt] = vbase + a;
+  }
+
+  // phase 1
+  v8 ka[N1];
+  v8 pf[4];
+#pragma unroll
+  for (int i = 0; i < R1; ++i) ka[i] = read_k<D, T>(kb, xk, i);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < N1; ++i) {
+    const int kt = i & 1, ks = i >> 1;
+    sn[kt] = mfma32(ka[i], x.qf[ks], i < 2 ? f32x16{} : sn[kt]);
+#pragma unroll
+    for (int j = 0; j < E1; ++j) {
+      const int idx = E1 * i + j;
+      const float p = fast_exp2(fmaf(score_at(sc, idx), x.c, -mc));
+      score_set(sc, idx, p);
+      if (idx & 1) {
+        pf[idx >> 3][(idx & 7) - 1] = static_cast<T>(score_at(sc, idx - 1));
+        pf[idx >> 3][idx & 7] = static_cast<T>(p);
+      }
+    }
+    if (i + R1 < N1) ka[i + R1] = read_k<D, T>(kb, xk, i + R1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // phase 2
+  v8 vt[N2];
+#pragma unroll
+  for (int i = 0; i < R2; ++i) vt[i] = read_vt<D, T>(vb[i % G::DT], i / G::DT);
+  float ps0 = 0.f, ps1 = 0.f, mx0 = -INFINITY, mx1 = -INFINITY;
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < N2; ++i) {
+    const int ks = i / G::DT, dt = i % G::DT;
+    o[dt] = mfma32(vt[i], pf[ks], o[dt]);
+    if (i < H2) {
+#pragma unroll
+      for (int j = 0; j < A2; j += 2) {
+        ps0 += score_at(sc, A2 * i + j);
+        ps1 += score_at(sc, A2 * i + j + 1);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < A2; j += 4) {
+        const int idx = A2 * (i - H2) + j;
+        mx0 = __builtin_fmaxf(__builtin_fmaxf(mx0, score_at(sn, idx)), score_at(sn, idx + 1));
+        mx1 = __builtin_fmaxf(__builtin_fmaxf(mx1, score_at(sn, idx + 2)), score_at(sn, idx + 3));
+      }
+    }
+    if (i + R2 < N2) vt[i + R2] = read_vt<D, T>(vb[(i + R2) % G::DT], (i + R2) / G::DT);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // keep the sums in this block (the compiler would otherwise sink them to
+  // their use after the slot, out of the MFMA shadow)
+  asm volatile("" : "+v"(ps0), "+v"(ps1), "+v"(mx0), "+v"(mx1));
+  l += ps0 + ps1;
+  return fmaxf(mx0, mx1);
+}
+
+// Per-wave view of one slot of the workgroup's plan.
+struct SlotInfo {
+  int j0;     // first key of the slot's tile
+  int act;    // SlotAction of this wave
+  Band band;  // band the action folds
+  bool mask;  // scores need masking
+};
+
+__device__ __forceinline__ SlotInfo slot_info(const Schedule& sc, int j0, bool repeat, int r0,
+                                              bool valid) {
+  SlotInfo s;
+  s.j0 = j0;
+  s.act = valid ? slot_action(sc, r0, j0, repeat) : kSkip;
+  const bool far = s.act == kBand2 || s.act == kFar;
+  s.band = far ? sc.p2 : sc.p1;
+  s.mask = s.act != kSkip && !wave_full(r0, s.band, j0);
+  return s;
+}
+
 template <int D, typename T, bool DUAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256),
-                          amdgpu_waves_per_eu(TTCD_WAVES_PER_EU, TTCD_WAVES_PER_EU)))
+__global__ __attribute__((amdgpu_flat_work_group_size(kWaves * 64, kWaves * 64),
+                          amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(AttnArgs a) {
   using G = Geo<D>;
   using v8 = typename VecT<T>::v8;
-  __shared__ __attribute__((aligned(16))) T smem[2 * G::STAGE];
+  __shared__ __attribute__((aligned(1024))) char smem_raw[G::NSTAGE * G::STAGE_B];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave / kGroupWaves;
+  const int sub = wave % kGroupWaves;
   const Schedule sc = a.sched;
   const int T_ = a.T;
 
-  // logical id order (b, kv head, q tile [heaviest first], head in group)
+  // Workgroup -> (b, kv head, query block [heaviest first], slice), XCD-remapped.
+  // Even GQA group: the two groups take heads 2*sl, 2*sl+1 of the group over
+  // one 128-token block. Otherwise: the two 128-token halves of a 256-token
+  // block of one head.
+  const bool paired = (a.G % 2) == 0;
+  const int nslice = paired ? a.G / 2 : a.G;
   int rest = xcd_remap(blockIdx.x, gridDim.x);
-  const int g = rest % a.G;
-  rest /= a.G;
+  const int sl = rest % nslice;
+  rest /= nslice;
   const int qb = a.nqb - 1 - rest % a.nqb;
   rest /= a.nqb;
   const int hk = rest % a.Hkv;
   const int b = rest / a.Hkv;
-  const int h = hk * a.G + g;
-
-  const int t0 = qb * kBlockM;
-  const int t_last = min(t0 + kBlockM, T_) - 1;
-  const int r0 = t0 + wave * kWaveRows;
-  const int qrow = r0 + (lane & 31);
+  const int span = paired ? kBlockM : 2 * kBlockM;
+  const int t0 = qb * span;
+  const int h = paired ? hk * a.G + 2 * sl + grp : hk * a.G + sl;
+  const int r0 = __builtin_amdgcn_readfirstlane(t0 + (paired ? 0 : grp * kBlockM) + sub * kWaveRows);
+  const int t_last = min(t0 + span, T_) - 1;
   const bool wave_valid = r0 < T_;
 
   const T* qp = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
   const T* kp = static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
   const T* vp = static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
-  T* ot = static_cast<T*>(a.o_t) + b * a.o_sb + h * a.o_sh;
-  T* os = DUAL ? static_cast<T*>(a.o_s) + b * a.o_sb + h * a.o_sh : nullptr;
-  float* lse_t = a.lse_t ? a.lse_t + ((int64_t)b * a.Hq + h) * T_ : nullptr;
-  float* lse_s = (DUAL && a.lse_s) ? a.lse_s + ((int64_t)b * a.Hq + h) * T_ : nullptr;
 
-  // Q^T operand fragments: lane holds query qrow, d = 16*ks + 8*(lane/32) + e.
-  v8 qf[G::DK];
+  Ctx<D, T> x;
+  x.lds = (LDS_AS char*)smem_raw;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)x.lds;
+  x.c = a.c;
+  x.qrow = r0 + (lane & 31);
+  x.half = lane >> 5;
+  x.T_ = T_;
+  x.ln = make_lane<D>(a.k_st, a.v_st, wave, lane);
   {
-    const T* src = qp + (int64_t)qrow * a.q_st + (lane >> 5) * 8;
+    const T* src = qp + (int64_t)x.qrow * a.q_st + (lane >> 5) * 8;
 #pragma unroll
     for (int ks = 0; ks < G::DK; ++ks) {
       v8 z = {};
-      qf[ks] = qrow < T_ ? *reinterpret_cast<const v8*>(src + ks * 16) : z;
+      x.qf[ks] = x.qrow < T_ ? *reinterpret_cast<const v8*>(src + ks * 16) : z;
     }
   }
-
-  f32x16 o[G::DT];
-#pragma unroll
-  for (int dt = 0; dt < G::DT; ++dt) o[dt] = f32x16{};
-  float m = -INFINITY, l = 0.f;
-  bool emitted_s = false;
 
   int n_hi = 0, n_lo = 1;
   if (!sc.wg_range(t0, t_last, &n_hi, &n_lo)) {
     n_hi = 0;
     n_lo = 1;
   }
+  const int count = n_hi - n_lo + 1;
+  const SlotPlan sp = make_slot_plan(
+      sc,
+      [&](int wv) {
+        return t0 + (paired ? 0 : (wv / kGroupWaves) * kBlockM) + (wv % kGroupWaves) * kWaveRows;
+      },
+      n_hi, n_lo);
+  // The plan is workgroup-uniform; keep it in scalar registers.
+  const int nslot = __builtin_amdgcn_readfirstlane(count > 0 ? sp.slots() : 0);
 
-  const LoadPlan<D> lp = make_load_plan<D>(a.k_st, a.v_st, wave, lane, tid);
-  VStage<D> vr;
-  if (n_hi >= n_lo) {
-    const int j0 = sc.tile_start(n_hi);
+  auto dma_slot = [&](int k, int j0) {
     const bool interior = j0 >= 0 && j0 + kBlockN <= T_;
-    issue_k_tile<D, T>(smem, kp, a.k_st, j0, T_, wave, lp, interior);
-    load_v_tile<D, T>(vr, vp, a.v_st, j0, T_, lp, interior);
-    store_v_tile<D, T>(vr, smem + G::K_ELEMS, tid);
+    const uint32_t st = lds_base + (k % G::NSTAGE) * G::STAGE_B;
+    dma_tile<D, T, true>(st, kp, a.k_st, j0, T_, wave, lane, x.ln.k_off, interior);
+    dma_tile<D, T, false>(st + G::TILE_B, vp, a.v_st, j0, T_, wave, lane, x.ln.v_off, interior);
+  };
+
+  f32x16 o[G::DT];
+#pragma unroll
+  for (int dt = 0; dt < G::DT; ++dt) o[dt] = f32x16{};
+  float m = -INFINITY, l = 0.f;
+  bool emitted_s = false;
+  f32x16 s0[2], s1[2];
+
+  // Prologue: slots 0, 1 and 2 in flight, scores of slot 0. The walker then
+  // stands at slot 3; (j1, rep1) and (j2, rep2) describe slots 1 and 2.
+  SlotWalker walk(sp);
+  walk.n = __builtin_amdgcn_readfirstlane(walk.n);
+#pragma unroll
+  for (int i = 0; i < kWalkDup; ++i) walk.d[i] = __builtin_amdgcn_readfirstlane(walk.d[i]);
+  const int j00 = sc.tile_start(walk.n);
+  const bool rep0 = walk.rep;
+  if (nslot > 0) dma_slot(0, j00);
+  walk.advance();
+  int j1 = sc.tile_start(walk.n);
+  bool rep1 = walk.rep;
+  if (nslot > 1) dma_slot(1, j1);
+  walk.advance();
+  int j2 = sc.tile_start(walk.n);
+  bool rep2 = walk.rep;
+  if (nslot > 2) dma_slot(2, j2);
+  walk.advance();
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  SlotInfo cur = slot_info(sc, j00, rep0, r0, wave_valid && nslot > 0);
+  float mx_next = -INFINITY;
+  {
+    s0[0] = f32x16{};
+    s0[1] = f32x16{};
+#pragma unroll
+    for (int i = 0; i < 2 * G::DK; ++i)
+      s0[i & 1] = mfma32(read_k<D, T>(x.lds, x.ln.xk, i), x.qf[i >> 1], s0[i & 1]);
+    if (cur.mask) mask_band(s0, x.qrow, cur.j0, T_, cur.band, x.half);
+    mx_next = cur.act != kSkip ? tile_max(s0) : -INFINITY;
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
 
-  for (int n = n_hi, it = 0; n >= n_lo; --n, ++it) {
-    T* ks = smem + (it & 1) * G::STAGE;
-    T* vt = ks + G::K_ELEMS;
-    T* nks = smem + ((it + 1) & 1) * G::STAGE;
-    const bool has_next = n - 1 >= n_lo;
-    if (has_next) {
-      const int jn = sc.tile_start(n - 1);
-      const bool interior = jn >= 0 && jn + kBlockN <= T_;
-      issue_k_tile<D, T>(nks, kp, a.k_st, jn, T_, wave, lp, interior);
-      load_v_tile<D, T>(vr, vp, a.v_st, jn, T_, lp, interior);
-    }
-
-    const int j0 = sc.tile_start(n);
-    if (wave_valid) {
-      const bool in1 = wave_touches(r0, sc.p1, j0);
-      const bool in2 = DUAL && wave_touches(r0, sc.p2, j0);
-      // At most two passes over the tile: phase 1 then (dual kernel, mixed
-      // tile only) phase 2, which recomputes S rather than keeping a copy.
-      int phase = in1 ? 1 : (in2 ? 2 : 0);
-      while (phase != 0) {
-        const Band band = phase == 1 ? sc.p1 : sc.p2;
-        f32x16 s[2];
-        compute_scores<D, T>(s, ks, qf, lane);
-        softmax_pv<D, T>(s, o, m, l, a.c, vt, lane, !wave_full(r0, band, j0), qrow, j0, T_,
-                         band);
-        if (DUAL && phase == 1 && wave_last(r0, sc.p1, j0)) {
-          emit<D, T>(o, m, l, a.c, os, a.o_st, lse_s, qrow, T_, lane);
-          emitted_s = true;
-        }
-        phase = (DUAL && phase == 1 && in2) ? 2 : 0;
+  // Slot k: the scores of slot k are in scur (row max mx_next); fold them and
+  // compute the scores of slot k+1 into snxt. Every slot runs the same code:
+  // a slot this wave skips folds all-zero probabilities. Unrolled by two so
+  // the two score buffers swap roles without register copies.
+  auto step = [&](f32x16 (&scur)[2], f32x16 (&snxt)[2], int k) {
+    const bool active = cur.act != kSkip;
+    // Reference max for slot k (lazy rescale), applied before its exp2.
+    if (active) {
+      const float m_new = fmaxf(m, mx_next);
+      const bool grow = m_new > m && (m == -INFINITY || (m_new - m) * x.c > kRescaleLog2);
+      if (__builtin_expect(__any(grow) != 0, 0)) {
+        const float mc_new = (m_new == -INFINITY) ? 0.f : m_new * x.c;
+        const float alpha = fast_exp2(fmaf(m, x.c, -mc_new));
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) o[dt] *= alpha;
+        m = m_new;
       }
     }
-    if (has_next) store_v_tile<D, T>(vr, nks + G::K_ELEMS, tid);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    const bool fetch = k + 3 < nslot;
+    const int j3 = sc.tile_start(walk.n);
+    const bool rep3 = walk.rep;
+    if (fetch) dma_slot(k + 3, j3);
+    walk.advance();
+    const SlotInfo nxt = slot_info(sc, j1, rep1, r0, wave_valid && k + 1 < nslot);
+    j1 = j2;
+    rep1 = rep2;
+    j2 = j3;
+    rep2 = rep3;
+    const float mc = active ? ((m == -INFINITY) ? 0.f : m * x.c) : INFINITY;
+    float mx = slot_body<D, T>(x, scur, snxt, o, l, mc,
+                               x.lds + ((k + 1) % G::NSTAGE) * G::STAGE_B,
+                               x.lds + (k % G::NSTAGE) * G::STAGE_B + G::TILE_B);
+    mx = xhalf_max(mx);
+    if (__builtin_expect(nxt.mask, 0)) {
+      mask_band(snxt, x.qrow, nxt.j0, T_, nxt.band, x.half);
+      mx = tile_max(snxt);
+    }
+    mx_next = nxt.act != kSkip ? mx : -INFINITY;
+    bool stored = false;
+    if (DUAL && cur.act == kStudentLast) {
+      T* os = static_cast<T*>(a.o_s) + b * a.o_sb + h * a.o_sh;
+      float* lse_s = a.lse_s ? a.lse_s + ((int64_t)b * a.Hq + h) * T_ : nullptr;
+      emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, lane);
+      emitted_s = true;
+      stored = true;
+    }
+    cur = nxt;
+    // Before the next slot, K of slot k+2 and V of slot k+1 must be in LDS:
+    // the loads of this slot (slot k+3) and the V loads of slot k+2 (issued
+    // last in the previous slot) may stay in flight. After output stores the
+    // count no longer isolates those loads: wait for everything.
+    if (stored) {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    } else if (fetch) {
+      if constexpr (G::NDMA == 2) asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory");
+    } else if (k + 2 < nslot) {
+      if constexpr (G::NDMA == 2) asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(1)\n\ts_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+  };
+
+  for (int k = 0; k < nslot; k += 2) {
+    step(s0, s1, k);
+    if (k + 1 < nslot) step(s1, s0, k + 1);
   }
 
   if (wave_valid) {
-    if (DUAL && !emitted_s) emit<D, T>(o, m, l, a.c, os, a.o_st, lse_s, qrow, T_, lane);
-    emit<D, T>(o, m, l, a.c, ot, a.o_st, lse_t, qrow, T_, lane);
+    if (DUAL && !emitted_s) {
+      T* os = static_cast<T*>(a.o_s) + b * a.o_sb + h * a.o_sh;
+      float* lse_s = a.lse_s ? a.lse_s + ((int64_t)b * a.Hq + h) * T_ : nullptr;
+      emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, lane);
+    }
+    T* ot = static_cast<T*>(a.o_t) + b * a.o_sb + h * a.o_sh;
+    float* lse_t = a.lse_t ? a.lse_t + ((int64_t)b * a.Hq + h) * T_ : nullptr;
+    emit<D, T>(o, m, l, x.c, ot, a.o_st, lse_t, x.qrow, T_, lane);
   }
 }
 
 template <int D, typename T, bool DUAL>
 hipError_t launch_typed(const AttnArgs& a, hipStream_t stream) {
-  const int grid = a.B * a.Hq * a.nqb;
+  const int nslice = (a.G % 2) == 0 ? a.G / 2 : a.G;
+  const int grid = a.B * a.Hkv * nslice * a.nqb;
   hipLaunchKernelGGL((attn_fwd_kernel<D, T, DUAL>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
   return hipGetLastError();
 }

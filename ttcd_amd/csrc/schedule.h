@@ -5,12 +5,15 @@
 // the exact iteration logic the GPU runs: every (query, key) pair inside a
 // window is folded into that window's output exactly once.
 //
-// Geometry. A workgroup owns kBlockM = 128 consecutive query tokens of one
-// query head; each of its 4 wavefronts owns 32 of them (rows r0..r0+31).
-// Keys are swept in tiles of kBlockN = 64, tile n covering keys
-// [64n - kshift, 64n - kshift + 63], from the tile holding the workgroup's
-// diagonal downward (the same backward-from-diagonal order as
-// profiling/fused_dual_attn.py:91,119,151,176,191).
+// Geometry. A workgroup has two groups of 4 wavefronts; each wavefront owns
+// 32 consecutive query rows (r0..r0+31) of one query head, so a group owns
+// kBlockM = 128 tokens. When the GQA group size is even the two groups take
+// two query heads sharing one K/V head over the same 128 tokens; otherwise
+// they take one head over 256 consecutive tokens. Keys are swept in tiles of
+// kBlockN = 64, tile n covering keys [64n - kshift, 64n - kshift + 63], from
+// the tile holding the workgroup's last diagonal downward (the same
+// backward-from-diagonal order as profiling/fused_dual_attn.py:91,119,151,
+// 176,191); every wave of the workgroup steps through the same tiles.
 //
 // Phases. A band {lo, hi} selects keys with lo <= i - j < hi. The dual kernel
 // runs phase 1 = student band {0, ws} and then phase 2 = far band {ws, wt}
@@ -26,7 +29,8 @@
 // [r0-ws+1, r0+31-ws]) to sit in one tile, so that all phase-1 tiles of a
 // wave precede all of its phase-2-only tiles. With r0 a multiple of 32 this
 // holds iff tile starts are congruent to (1 - ws) or (-ws) modulo 32, hence
-// kshift = ws mod 32 for the dual kernel (0 for single-band calls).
+// kshift = ws mod 32 for the dual kernel (0 for single-band calls). It also
+// makes the two waves of each aligned 64-row pair share their mixed tile.
 #pragma once
 
 #include <stdint.h>
@@ -41,8 +45,9 @@ namespace ttcd {
 
 constexpr int kBlockN = 64;    // keys per K/V tile
 constexpr int kWaveRows = 32;  // query rows per wavefront
-constexpr int kWaves = 4;      // wavefronts per workgroup
-constexpr int kBlockM = kWaveRows * kWaves;  // query tokens per workgroup
+constexpr int kGroupWaves = 4;  // wavefronts per group
+constexpr int kWaves = 2 * kGroupWaves;  // wavefronts per workgroup
+constexpr int kBlockM = kWaveRows * kGroupWaves;  // query tokens per group
 
 struct Band {
   int lo;  // inclusive lower bound of i - j
@@ -98,6 +103,141 @@ TTCD_HD bool visible(int i, int j, Band b, int T) {
   const int d = i - j;
   return d >= b.lo && d < b.hi && j >= 0 && j < T;
 }
+
+// Slots. A workgroup sweeps a sequence of slots, one tile per slot. For the
+// dual kernel each distinct "mixed" tile of its waves (a tile holding both
+// student and far keys of a wave, at most one per wave) appears twice in a
+// row: in the first slot its waves fold the student keys and then write the
+// student output; in the repeated slot they fold the far keys. Waves whose
+// mixed tile it is not skip the repeated slot. Every wave therefore carries
+// one accumulator and one pending P^T between phases, as in the band kernel.
+constexpr int kMaxDup = 2 * kGroupWaves;
+constexpr int kNoTile = -0x7fffffff - 1;
+
+// All loops below have compile-time trip counts and static indices, so on the
+// GPU the plan lives in scalar registers (no scratch memory).
+struct SlotPlan {
+  int n_hi;            // first (highest) tile
+  int count;           // tiles n_hi .. n_hi - count + 1
+  int ndup;            // repeated (mixed) tiles
+  int dup[kMaxDup];    // their tile indices, descending; kNoTile for unused entries
+
+  TTCD_HD int slots() const { return count + ndup; }
+
+  // Tile of slot k and whether it is a repeat.
+  TTCD_HD int tile(int k, bool* repeat) const {
+    int n = n_hi - k;
+    int before = 0;       // repeats already placed
+    int rep_tile = kNoTile;
+#pragma unroll
+    for (int i = 0; i < kMaxDup; ++i) {
+      if (dup[i] != kNoTile) {
+        const int first = n_hi - dup[i] + before;  // slot of dup[i]'s first pass
+        if (k == first + 1) rep_tile = dup[i];
+        if (k > first + 1) n += 1;
+        before += 1;
+      }
+    }
+    *repeat = rep_tile != kNoTile;
+    return *repeat ? rep_tile : n;
+  }
+};
+
+// The wave's mixed tile, or kNoTile when it has none.
+TTCD_HD int wave_mixed_tile(const Schedule& sc, int r0) {
+  if (!sc.dual) return kNoTile;
+  int lowest = r0 - sc.p1.hi + 1;  // lowest student key of the wave
+  if (lowest < 0) lowest = 0;
+  const int n = sc.tile_of(lowest);
+  const int j0 = sc.tile_start(n);
+  return (wave_touches(r0, sc.p1, j0) && wave_touches(r0, sc.p2, j0)) ? n : kNoTile;
+}
+
+// Slot plan of a workgroup whose wave w starts at row r0_of_wave(w) (rows >= T
+// are idle waves) and whose tiles are n_hi down to n_lo.
+template <typename R0>
+TTCD_HD SlotPlan make_slot_plan(const Schedule& sc, R0 r0_of_wave, int n_hi, int n_lo) {
+  SlotPlan sp;
+  sp.n_hi = n_hi;
+  sp.count = n_hi - n_lo + 1;
+  int* d = sp.dup;
+#pragma unroll
+  for (int w = 0; w < kMaxDup; ++w) {
+    const int r0 = r0_of_wave(w);
+    const int n = r0 < sc.T ? wave_mixed_tile(sc, r0) : kNoTile;
+    d[w] = (n >= n_lo && n <= n_hi) ? n : kNoTile;
+  }
+  // sort descending (kNoTile is the smallest int), blank out repeats, then
+  // sort again so the distinct tiles lead the array
+  auto sort_desc = [](int* v) {
+#pragma unroll
+    for (int a = 0; a < kMaxDup; ++a)
+#pragma unroll
+      for (int b = 0; b + 1 < kMaxDup - a; ++b)
+        if (v[b] < v[b + 1]) {
+          const int t = v[b];
+          v[b] = v[b + 1];
+          v[b + 1] = t;
+        }
+  };
+  sort_desc(d);
+  sp.ndup = 0;
+  int prev = kNoTile;
+#pragma unroll
+  for (int i = 0; i < kMaxDup; ++i) {
+    const int v = d[i];
+    d[i] = (v == prev) ? kNoTile : v;
+    prev = v;
+    sp.ndup += d[i] != kNoTile;
+  }
+  sort_desc(d);
+  return sp;
+}
+
+// Distinct repeated tiles a plan can hold: at most one per wave (the two
+// waves of an aligned 64-row pair share theirs only when ws mod 64 < 32).
+constexpr int kWalkDup = kMaxDup;
+
+// Walks the slots of a plan in order with O(1) work per slot: the current
+// tile, whether the slot repeats the previous tile, and the remaining
+// repeated tiles (descending; consumed from the front).
+struct SlotWalker {
+  int n;
+  bool rep;
+  int d[kWalkDup];
+
+  TTCD_HD explicit SlotWalker(const SlotPlan& sp) : n(sp.n_hi), rep(false) {
+#pragma unroll
+    for (int i = 0; i < kWalkDup; ++i) d[i] = sp.dup[i];
+  }
+  TTCD_HD void advance() {
+    if (!rep && n == d[0]) {
+      rep = true;
+#pragma unroll
+      for (int i = 0; i + 1 < kWalkDup; ++i) d[i] = d[i + 1];
+      d[kWalkDup - 1] = kNoTile;
+    } else {
+      rep = false;
+      n -= 1;
+    }
+  }
+};
+
+// What a wave folds in a slot: nothing, one band (mask chosen by wave_full),
+// the student part of its mixed tile (then writes the student output) or the
+// far part (repeat slot).
+enum SlotAction { kSkip = 0, kBand1 = 1, kBand2 = 2, kStudentLast = 3, kFar = 4 };
+
+TTCD_HD int slot_action(const Schedule& sc, int r0, int j0, bool repeat) {
+  const bool in1 = wave_touches(r0, sc.p1, j0);
+  const bool in2 = sc.dual && wave_touches(r0, sc.p2, j0);
+  if (repeat) return (in1 && in2) ? kFar : kSkip;
+  if (in1 && (in2 || (sc.dual && wave_last(r0, sc.p1, j0)))) return kStudentLast;
+  return in1 ? kBand1 : (in2 ? kBand2 : kSkip);
+}
+
+// Query tokens swept by one workgroup for a GQA group size (see Geometry).
+TTCD_HD int wg_span_tokens(int gqa_group) { return gqa_group % 2 == 0 ? kBlockM : 2 * kBlockM; }
 
 // Schedules built by the C ABI entry points (windows already validated).
 TTCD_HD Schedule make_dual_schedule(int T, int ws, int wt) {
