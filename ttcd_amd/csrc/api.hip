@@ -226,11 +226,10 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
       return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi");
     sc = make_band_schedule(T, window_s, window_t);
   }
-  // Workgroup geometry as launched (attn.hip): both groups over the same 128
-  // tokens (two heads) for an even GQA group, else the two groups over the
-  // halves of 256 tokens of one head. The slice's rows are owned by the waves
-  // r0 = t0 + 32*w for w < span/32; the slot plan is built from all 8 waves.
-  const bool paired = gqa_group % 2 == 0;
+  // Workgroup geometry as launched (attn.hip): 4 waves over 128 consecutive
+  // tokens of one head, wave w owning rows r0 = t0 + 32*w (gqa_group does not
+  // change it).
+  (void)gqa_group;
   const int span = wg_span_tokens(gqa_group);
   const int nwg = (T + span - 1) / span;
   for (int qb = 0; qb < nwg; ++qb) {
@@ -238,9 +237,7 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
     const int t_last = (t0 + span < T ? t0 + span : T) - 1;
     int n_hi, n_lo;
     if (!sc.wg_range(t0, t_last, &n_hi, &n_lo)) continue;
-    auto r0_of_wave = [&](int wv) {
-      return t0 + (paired ? 0 : (wv / kGroupWaves) * kBlockM) + (wv % kGroupWaves) * kWaveRows;
-    };
+    auto r0_of_wave = [&](int wv) { return t0 + wv * kWaveRows; };
     const SlotPlan sp = make_slot_plan(sc, r0_of_wave, n_hi, n_lo);
     if (sp.ndup > kWalkDup)
       return fail(TTCD_ERR_UNSUPPORTED, "schedule error: %d repeated tiles > %d", sp.ndup, kWalkDup);
@@ -257,6 +254,15 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
                       walk.n, (int)walk.rep, n, (int)repeat, k);
         const int j0 = sc.tile_start(n);
         const int act = slot_action(sc, r0, j0, repeat);
+        const WaveSlots ws(sc, r0);  // the kernel's closed form
+        if (ws.act(n, repeat) != act)
+          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: closed-form action %d != %d (r0=%d n=%d)",
+                      ws.act(n, repeat), act, r0, n);
+        if (act != kSkip) {
+          const Band b = (act == kBand2 || act == kFar) ? sc.p2 : sc.p1;
+          if (ws.mask(n, act) != !wave_full(r0, b, j0))
+            return fail(TTCD_ERR_UNSUPPORTED, "schedule error: closed-form mask (r0=%d n=%d)", r0, n);
+        }
         if (act == kSkip) continue;
         const bool far = act == kBand2 || act == kFar;
         if (sc.dual && !far && student_done)

@@ -120,7 +120,7 @@ struct Geo {
   static constexpr int CPR = D / 8;                // 16-byte chunks per row
   static constexpr int TILE_B = kBlockN * RB;      // bytes of one K or V tile
   static constexpr int STAGE_B = 2 * TILE_B;       // K tile, then V tile
-  static constexpr int NSTAGE = 4;                 // tile k+3 loads while k+1 / k are read
+  static constexpr int NSTAGE = 2;                 // K and V halves refilled one slot ahead
   static constexpr int DK = D / 16;                // MFMA k-steps of S^T = K Q^T
   static constexpr int DT = D / 32;                // 32-row d tiles of O^T
   static constexpr int NTH = kWaves * 64;
@@ -335,25 +335,28 @@ __device__ __forceinline__ void score_set(f32x16 (&s)[2], int idx, float v) {
 
 // One slot of the software pipeline, in issue order (sched_barrier fences
 // keep the compiler from regrouping it):
-//   phase 1: the scores S(k+1) from the K tile at kb (2*DK MFMAs), with the
-//            exp2 / bf16 packing of S(k) spread between them and the K
-//            operand reads R1 MFMAs ahead;
+//   phase 1: the scores S(k+1) from the K tile at kb (2*DK MFMAs). After the
+//            first two, settle() masks S(k) if needed, settles the reference
+//            max of slot k (rescaling O^T when it moves) and returns m*c for
+//            its exp2 (+inf for a slot this wave skips); the exp2 / bf16
+//            packing of S(k) is then spread over the remaining MFMAs. K
+//            operand reads run R1 MFMAs ahead. side(i) runs after MFMA i.
 //   phase 2: PV(k) from the V tile at vbase (4*DT MFMAs), with the row sum of
 //            S(k) and then the row max of S(k+1) spread between them and the
 //            V^T operand reads R2 MFMAs ahead.
-// mc = +inf turns every p of S(k) into exactly 0 (a slot this wave skips).
 // Returns this lane's (unmasked) max of S(k+1), not yet combined across halves.
-template <int D, typename T>
+template <int D, typename T, typename Settle, typename Side>
 __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], f32x16 (&sn)[2],
-                                           f32x16 (&o)[Geo<D>::DT], float& l, float mc,
-                                           const LDS_AS char* kb, const LDS_AS char* vbase) {
+                                           f32x16 (&o)[Geo<D>::DT], float& l,
+                                           const LDS_AS char* kb, const LDS_AS char* vbase,
+                                           Settle&& settle, Side&& side) {
   using G = Geo<D>;
   using v8 = typename VecT<T>::v8;
   constexpr int N1 = 2 * G::DK;  // score MFMAs
   constexpr int N2 = 4 * G::DT;  // PV MFMAs
   constexpr int R1 = 3;
   constexpr int R2 = 2;
-  constexpr int E1 = 32 / N1;    // scores exponentiated per score MFMA
+  constexpr int P1 = 2;          // score MFMAs issued before settle()
   constexpr int H2 = N2 / 2;     // PV MFMAs carrying sums (the rest carry maxima)
   constexpr int A2 = 32 / H2;    // values summed / maxed per PV MFMA
 
@@ -372,6 +375,7 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
   // phase 1
   v8 ka[N1];
   v8 pf[4];
+  float mc = 0.f;
 #pragma unroll
   for (int i = 0; i < R1; ++i) ka[i] = read_k<D, T>(kb, xk, i);
   __builtin_amdgcn_sched_barrier(0);
@@ -379,17 +383,22 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
   for (int i = 0; i < N1; ++i) {
     const int kt = i & 1, ks = i >> 1;
     sn[kt] = mfma32(ka[i], x.qf[ks], i < 2 ? f32x16{} : sn[kt]);
+    if (i + R1 < N1) ka[i + R1] = read_k<D, T>(kb, xk, i + R1);
+    if (i == P1 - 1) mc = settle();
+    if (i >= P1) {
+      // scores (32 * (i - P1) / (N1 - P1)) .. (32 * (i + 1 - P1) / (N1 - P1)) - 1
+      const int e0 = 32 * (i - P1) / (N1 - P1), e1 = 32 * (i + 1 - P1) / (N1 - P1);
 #pragma unroll
-    for (int j = 0; j < E1; ++j) {
-      const int idx = E1 * i + j;
-      const float p = fast_exp2(fmaf(score_at(sc, idx), x.c, -mc));
-      score_set(sc, idx, p);
-      if (idx & 1) {
-        pf[idx >> 3][(idx & 7) - 1] = static_cast<T>(score_at(sc, idx - 1));
-        pf[idx >> 3][idx & 7] = static_cast<T>(p);
+      for (int idx = e0; idx < e1; ++idx) {
+        const float p = fast_exp2(fmaf(score_at(sc, idx), x.c, -mc));
+        score_set(sc, idx, p);
+        if (idx & 1) {
+          pf[idx >> 3][(idx & 7) - 1] = static_cast<T>(score_at(sc, idx - 1));
+          pf[idx >> 3][idx & 7] = static_cast<T>(p);
+        }
       }
     }
-    if (i + R1 < N1) ka[i + R1] = read_k<D, T>(kb, xk, i + R1);
+    side(i);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -435,15 +444,24 @@ struct SlotInfo {
   bool mask;  // scores need masking
 };
 
-__device__ __forceinline__ SlotInfo slot_info(const Schedule& sc, int j0, bool repeat, int r0,
-                                              bool valid) {
+__device__ __forceinline__ SlotInfo slot_info(const Schedule& sc, const WaveSlots& ws, int n,
+                                              bool repeat, bool valid) {
   SlotInfo s;
-  s.j0 = j0;
-  s.act = valid ? slot_action(sc, r0, j0, repeat) : kSkip;
-  const bool far = s.act == kBand2 || s.act == kFar;
+  s.j0 = sc.tile_start(n);
+  s.act = valid ? ws.act(n, repeat) : (int)kSkip;
+  const bool far = (s.act == kBand2) | (s.act == kFar);
   s.band = far ? sc.p2 : sc.p1;
-  s.mask = s.act != kSkip && !wave_full(r0, s.band, j0);
+  s.mask = (s.act != kSkip) & ws.mask(n, s.act);
   return s;
+}
+
+// A wave-uniform 64-bit pointer held in scalar registers.
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+  const uint64_t b = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  return reinterpret_cast<const T*>((uint64_t)lo | ((uint64_t)hi << 32));
 }
 
 template <int D, typename T, bool DUAL>
@@ -457,34 +475,28 @@ void attn_fwd_kernel(AttnArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave / kGroupWaves;
-  const int sub = wave % kGroupWaves;
   const Schedule sc = a.sched;
   const int T_ = a.T;
 
-  // Workgroup -> (b, kv head, query block [heaviest first], slice), XCD-remapped.
-  // Even GQA group: the two groups take heads 2*sl, 2*sl+1 of the group over
-  // one 128-token block. Otherwise: the two 128-token halves of a 256-token
-  // block of one head.
-  const bool paired = (a.G % 2) == 0;
-  const int nslice = paired ? a.G / 2 : a.G;
+  // Workgroup -> (b, kv head, query block [heaviest first], head in group),
+  // XCD-remapped: each XCD sweeps a contiguous run, so the query heads
+  // sharing a K/V head and neighbouring query blocks share its L2.
   int rest = xcd_remap(blockIdx.x, gridDim.x);
-  const int sl = rest % nslice;
-  rest /= nslice;
+  const int g = rest % a.G;
+  rest /= a.G;
   const int qb = a.nqb - 1 - rest % a.nqb;
   rest /= a.nqb;
   const int hk = rest % a.Hkv;
   const int b = rest / a.Hkv;
-  const int span = paired ? kBlockM : 2 * kBlockM;
-  const int t0 = qb * span;
-  const int h = paired ? hk * a.G + 2 * sl + grp : hk * a.G + sl;
-  const int r0 = __builtin_amdgcn_readfirstlane(t0 + (paired ? 0 : grp * kBlockM) + sub * kWaveRows);
-  const int t_last = min(t0 + span, T_) - 1;
+  const int h = hk * a.G + g;
+  const int t0 = qb * kBlockM;
+  const int r0 = __builtin_amdgcn_readfirstlane(t0 + wave * kWaveRows);
+  const int t_last = min(t0 + kBlockM, T_) - 1;
   const bool wave_valid = r0 < T_;
 
   const T* qp = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
-  const T* kp = static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
-  const T* vp = static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
+  const T* kp = uniform_ptr(static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh);
+  const T* vp = uniform_ptr(static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh);
 
   Ctx<D, T> x;
   x.lds = (LDS_AS char*)smem_raw;
@@ -510,19 +522,28 @@ void attn_fwd_kernel(AttnArgs a) {
   }
   const int count = n_hi - n_lo + 1;
   const SlotPlan sp = make_slot_plan(
-      sc,
-      [&](int wv) {
-        return t0 + (paired ? 0 : (wv / kGroupWaves) * kBlockM) + (wv % kGroupWaves) * kWaveRows;
-      },
-      n_hi, n_lo);
+      sc, [&](int wv) { return t0 + wv * kWaveRows; }, n_hi, n_lo);
   // The plan is workgroup-uniform; keep it in scalar registers.
   const int nslot = __builtin_amdgcn_readfirstlane(count > 0 ? sp.slots() : 0);
 
-  auto dma_slot = [&](int k, int j0) {
-    const bool interior = j0 >= 0 && j0 + kBlockN <= T_;
-    const uint32_t st = lds_base + (k % G::NSTAGE) * G::STAGE_B;
-    dma_tile<D, T, true>(st, kp, a.k_st, j0, T_, wave, lane, x.ln.k_off, interior);
-    dma_tile<D, T, false>(st + G::TILE_B, vp, a.v_st, j0, T_, wave, lane, x.ln.v_off, interior);
+  const WaveSlots wsl(sc, r0);
+  const int64_t kst = a.k_st, vst = a.v_st;
+  // DMA of the K (or V) tile of tile index n into the K (V) half of stage s.
+  auto dma_half = [&](bool is_k, int n, int s) {
+    const int j0 = sc.tile_start(n);
+    const uint32_t dst = lds_base + s * G::STAGE_B + (is_k ? 0 : G::TILE_B);
+    const T* base = is_k ? kp : vp;
+    const int64_t st = is_k ? kst : vst;
+    if (__builtin_expect((j0 >= 0) & (j0 + kBlockN <= T_), 1)) {
+#pragma unroll
+      for (int i = 0; i < G::NDMA; ++i)
+        dma16(base + (int64_t)j0 * st, is_k ? x.ln.k_off[i] : x.ln.v_off[i],
+              dst + (wave + kWaves * i) * 1024);
+    } else if (is_k) {
+      dma_tile<D, T, true>(dst, kp, kst, j0, T_, wave, lane, x.ln.k_off, false);
+    } else {
+      dma_tile<D, T, false>(dst, vp, vst, j0, T_, wave, lane, x.ln.v_off, false);
+    }
   };
 
   f32x16 o[G::DT];
@@ -532,47 +553,79 @@ void attn_fwd_kernel(AttnArgs a) {
   bool emitted_s = false;
   f32x16 s0[2], s1[2];
 
-  // Prologue: slots 0, 1 and 2 in flight, scores of slot 0. The walker then
-  // stands at slot 3; (j1, rep1) and (j2, rep2) describe slots 1 and 2.
+  // Two stages; stage k % 2 holds K(k) and V(k). In slot k the scores read
+  // K(k+1) and PV reads V(k), so K(k+2) can replace K(k) (read in slot k-1)
+  // and V(k+1) can replace V(k-1): both are fetched at the start of slot k
+  // and have the whole slot to land.
+  // Prologue: K(0), V(0), K(1) in LDS, scores of slot 0. The walker then
+  // stands at slot 2; (n1, rep1) describes slot 1.
   SlotWalker walk(sp);
   walk.n = __builtin_amdgcn_readfirstlane(walk.n);
 #pragma unroll
   for (int i = 0; i < kWalkDup; ++i) walk.d[i] = __builtin_amdgcn_readfirstlane(walk.d[i]);
-  const int j00 = sc.tile_start(walk.n);
+  const int n0 = walk.n;
   const bool rep0 = walk.rep;
-  if (nslot > 0) dma_slot(0, j00);
+  if (nslot > 0) {
+    dma_half(true, n0, 0);
+    dma_half(false, n0, 0);
+  }
   walk.advance();
-  int j1 = sc.tile_start(walk.n);
+  int n1 = walk.n;
   bool rep1 = walk.rep;
-  if (nslot > 1) dma_slot(1, j1);
-  walk.advance();
-  int j2 = sc.tile_start(walk.n);
-  bool rep2 = walk.rep;
-  if (nslot > 2) dma_slot(2, j2);
+  if (nslot > 1) dma_half(true, n1, 1);
   walk.advance();
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  SlotInfo cur = slot_info(sc, j00, rep0, r0, wave_valid && nslot > 0);
-  float mx_next = -INFINITY;
+  SlotInfo cur = slot_info(sc, wsl, n0, rep0, wave_valid && nslot > 0);
+  // Scores of slot 0 and their lane max (unmasked; slot 0's mask and
+  // reference max are settled inside the first slot).
+  float mx_lane;
   {
     s0[0] = f32x16{};
     s0[1] = f32x16{};
 #pragma unroll
     for (int i = 0; i < 2 * G::DK; ++i)
       s0[i & 1] = mfma32(read_k<D, T>(x.lds, x.ln.xk, i), x.qf[i >> 1], s0[i & 1]);
-    if (cur.mask) mask_band(s0, x.qrow, cur.j0, T_, cur.band, x.half);
-    mx_next = cur.act != kSkip ? tile_max(s0) : -INFINITY;
+    float a0 = -INFINITY, a1 = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      a0 = fmaxf(a0, s0[0][e]);
+      a1 = fmaxf(a1, s0[1][e]);
+    }
+    mx_lane = fmaxf(a0, a1);
   }
+  // every wave has read K(0) before slot 0 replaces it with K(2)
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  // Slot k: the scores of slot k are in scur (row max mx_next); fold them and
-  // compute the scores of slot k+1 into snxt. Every slot runs the same code:
-  // a slot this wave skips folds all-zero probabilities. Unrolled by two so
-  // the two score buffers swap roles without register copies.
+  // Slot k: the scores of slot k are in scur (lane max mx_lane, not yet
+  // masked); fold them and compute the scores of slot k+1 into snxt. Every
+  // slot runs the same code: a slot this wave skips folds all-zero
+  // probabilities. Unrolled by two so the two score buffers swap roles
+  // without register copies.
   auto step = [&](f32x16 (&scur)[2], f32x16 (&snxt)[2], int k) {
-    const bool active = cur.act != kSkip;
-    // Reference max for slot k (lazy rescale), applied before its exp2.
-    if (active) {
-      const float m_new = fmaxf(m, mx_next);
-      const bool grow = m_new > m && (m == -INFINITY || (m_new - m) * x.c > kRescaleLog2);
+    const int n2 = walk.n;
+    const bool rep2 = walk.rep;
+    if (k + 2 < nslot) dma_half(true, n2, k & 1);
+    if (k + 1 < nslot) dma_half(false, n1, (k + 1) & 1);
+    SlotInfo nxt;
+    // Mask S(k) if needed, then the reference max of slot k (lazy rescale):
+    // moved, and O^T / l rescaled, only when some row's max exceeds it by
+    // more than 2^kRescaleLog2. Returns m*c for the exp2 of slot k.
+    auto settle = [&]() {
+      float mx = mx_lane;
+      if (__builtin_expect(cur.mask, 0)) {
+        mask_band(scur, x.qrow, cur.j0, T_, cur.band, x.half);
+        float a0 = -INFINITY, a1 = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          a0 = fmaxf(a0, scur[0][e]);
+          a1 = fmaxf(a1, scur[1][e]);
+        }
+        mx = fmaxf(a0, a1);
+      }
+      mx = xhalf_max(mx);
+      const bool active = cur.act != kSkip;
+      const float m_new = active ? fmaxf(m, mx) : m;
+      const bool grow = (m_new > m) & ((m == -INFINITY) | ((m_new - m) * x.c > kRescaleLog2));
       if (__builtin_expect(__any(grow) != 0, 0)) {
         const float mc_new = (m_new == -INFINITY) ? 0.f : m_new * x.c;
         const float alpha = fast_exp2(fmaf(m, x.c, -mc_new));
@@ -581,27 +634,13 @@ void attn_fwd_kernel(AttnArgs a) {
         for (int dt = 0; dt < G::DT; ++dt) o[dt] *= alpha;
         m = m_new;
       }
-    }
-    const bool fetch = k + 3 < nslot;
-    const int j3 = sc.tile_start(walk.n);
-    const bool rep3 = walk.rep;
-    if (fetch) dma_slot(k + 3, j3);
-    walk.advance();
-    const SlotInfo nxt = slot_info(sc, j1, rep1, r0, wave_valid && k + 1 < nslot);
-    j1 = j2;
-    rep1 = rep2;
-    j2 = j3;
-    rep2 = rep3;
-    const float mc = active ? ((m == -INFINITY) ? 0.f : m * x.c) : INFINITY;
-    float mx = slot_body<D, T>(x, scur, snxt, o, l, mc,
-                               x.lds + ((k + 1) % G::NSTAGE) * G::STAGE_B,
-                               x.lds + (k % G::NSTAGE) * G::STAGE_B + G::TILE_B);
-    mx = xhalf_max(mx);
-    if (__builtin_expect(nxt.mask, 0)) {
-      mask_band(snxt, x.qrow, nxt.j0, T_, nxt.band, x.half);
-      mx = tile_max(snxt);
-    }
-    mx_next = nxt.act != kSkip ? mx : -INFINITY;
+      return active ? ((m == -INFINITY) ? 0.f : m * x.c) : INFINITY;
+    };
+    auto side = [&](int i) {
+      if (i == 2) nxt = slot_info(sc, wsl, n1, rep1, wave_valid & (k + 1 < nslot));
+    };
+    mx_lane = slot_body<D, T>(x, scur, snxt, o, l, x.lds + ((k + 1) & 1) * G::STAGE_B,
+                              x.lds + (k & 1) * G::STAGE_B + G::TILE_B, settle, side);
     bool stored = false;
     if (DUAL && cur.act == kStudentLast) {
       T* os = static_cast<T*>(a.o_s) + b * a.o_sb + h * a.o_sh;
@@ -611,21 +650,11 @@ void attn_fwd_kernel(AttnArgs a) {
       stored = true;
     }
     cur = nxt;
-    // Before the next slot, K of slot k+2 and V of slot k+1 must be in LDS:
-    // the loads of this slot (slot k+3) and the V loads of slot k+2 (issued
-    // last in the previous slot) may stay in flight. After output stores the
-    // count no longer isolates those loads: wait for everything.
-    if (stored) {
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    } else if (fetch) {
-      if constexpr (G::NDMA == 2) asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory");
-    } else if (k + 2 < nslot) {
-      if constexpr (G::NDMA == 2) asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(1)\n\ts_barrier" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    }
+    walk.advance();
+    n1 = n2;
+    rep1 = rep2;
+    // K(k+2) and V(k+1), fetched at the start of this slot, are read in the next.
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   };
 
   for (int k = 0; k < nslot; k += 2) {
@@ -647,8 +676,7 @@ void attn_fwd_kernel(AttnArgs a) {
 
 template <int D, typename T, bool DUAL>
 hipError_t launch_typed(const AttnArgs& a, hipStream_t stream) {
-  const int nslice = (a.G % 2) == 0 ? a.G / 2 : a.G;
-  const int grid = a.B * a.Hkv * nslice * a.nqb;
+  const int grid = a.B * a.Hq * a.nqb;
   hipLaunchKernelGGL((attn_fwd_kernel<D, T, DUAL>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
   return hipGetLastError();
 }

@@ -5,15 +5,13 @@
 // the exact iteration logic the GPU runs: every (query, key) pair inside a
 // window is folded into that window's output exactly once.
 //
-// Geometry. A workgroup has two groups of 4 wavefronts; each wavefront owns
-// 32 consecutive query rows (r0..r0+31) of one query head, so a group owns
-// kBlockM = 128 tokens. When the GQA group size is even the two groups take
-// two query heads sharing one K/V head over the same 128 tokens; otherwise
-// they take one head over 256 consecutive tokens. Keys are swept in tiles of
-// kBlockN = 64, tile n covering keys [64n - kshift, 64n - kshift + 63], from
-// the tile holding the workgroup's last diagonal downward (the same
-// backward-from-diagonal order as profiling/fused_dual_attn.py:91,119,151,
-// 176,191); every wave of the workgroup steps through the same tiles.
+// Geometry. A workgroup has 4 wavefronts; each wavefront owns 32 consecutive
+// query rows (r0..r0+31) of one query head, so a workgroup owns kBlockM = 128
+// tokens of one head. Keys are swept in tiles of kBlockN = 64, tile n
+// covering keys [64n - kshift, 64n - kshift + 63], from the tile holding the
+// workgroup's last diagonal downward (the same backward-from-diagonal order
+// as profiling/fused_dual_attn.py:91,119,151,176,191); every wave of the
+// workgroup steps through the same tiles.
 //
 // Phases. A band {lo, hi} selects keys with lo <= i - j < hi. The dual kernel
 // runs phase 1 = student band {0, ws} and then phase 2 = far band {ws, wt}
@@ -45,9 +43,8 @@ namespace ttcd {
 
 constexpr int kBlockN = 64;    // keys per K/V tile
 constexpr int kWaveRows = 32;  // query rows per wavefront
-constexpr int kGroupWaves = 4;  // wavefronts per group
-constexpr int kWaves = 2 * kGroupWaves;  // wavefronts per workgroup
-constexpr int kBlockM = kWaveRows * kGroupWaves;  // query tokens per group
+constexpr int kWaves = 4;      // wavefronts per workgroup
+constexpr int kBlockM = kWaveRows * kWaves;  // query tokens per workgroup
 
 struct Band {
   int lo;  // inclusive lower bound of i - j
@@ -111,7 +108,7 @@ TTCD_HD bool visible(int i, int j, Band b, int T) {
 // student output; in the repeated slot they fold the far keys. Waves whose
 // mixed tile it is not skip the repeated slot. Every wave therefore carries
 // one accumulator and one pending P^T between phases, as in the band kernel.
-constexpr int kMaxDup = 2 * kGroupWaves;
+constexpr int kMaxDup = kWaves;
 constexpr int kNoTile = -0x7fffffff - 1;
 
 // All loops below have compile-time trip counts and static indices, so on the
@@ -236,8 +233,69 @@ TTCD_HD int slot_action(const Schedule& sc, int r0, int j0, bool repeat) {
   return in1 ? kBand1 : (in2 ? kBand2 : kSkip);
 }
 
-// Query tokens swept by one workgroup for a GQA group size (see Geometry).
-TTCD_HD int wg_span_tokens(int gqa_group) { return gqa_group % 2 == 0 ? kBlockM : 2 * kBlockM; }
+// Per-wave slot actions in closed form: the tile-index ranges behind
+// slot_action() and wave_full(), computed once per wave so that each slot
+// costs a few branch-free scalar compares. Must agree with those functions
+// on every tile of the sweep (checked by ttcd_attn_schedule_coverage).
+struct WaveSlots {
+  int n1a, n1b;  // tiles touched by phase 1 (empty: n1a > n1b)
+  int n2a, n2b;  // tiles touched by phase 2 (dual kernel)
+  int nl;        // tiles n <= nl end the student phase (wave_last)
+  int f1a, f1b;  // tiles fully inside band 1
+  int f2a, f2b;  // tiles fully inside band 2
+  int dual;
+
+  TTCD_HD WaveSlots(const Schedule& sc, int r0) : dual(sc.dual) {
+    const int big = 0x3fffffff;
+    auto range = [&](Band b, int* a, int* z) {
+      if (b.lo < b.hi) {
+        *a = sc.tile_of(r0 - b.hi + 1);
+        *z = sc.tile_of(r0 + kWaveRows - 1 - b.lo);
+      } else {
+        *a = big;
+        *z = -big;
+      }
+    };
+    range(sc.p1, &n1a, &n1b);
+    if (sc.dual) {
+      range(sc.p2, &n2a, &n2b);
+    } else {
+      n2a = big;
+      n2b = -big;
+    }
+    const int lowest = r0 - sc.p1.hi + 1;
+    nl = sc.tile_of(lowest > 0 ? lowest : 0);
+    const int nz = sc.kshift > 0 ? 1 : 0;  // first tile with j0 >= 0
+    auto full = [&](Band b, int* a, int* z) {
+      const int lo_t = sc.tile_of(r0 + kWaveRows + kBlockN - 1 - b.hi);  // j0 > r0 + 31 - hi
+      *a = lo_t > nz ? lo_t : nz;
+      *z = sc.tile_of(r0 - (kBlockN - 1) - b.lo);                      // j0 <= r0 - 63 - lo
+    };
+    full(sc.p1, &f1a, &f1b);
+    full(sc.p2, &f2a, &f2b);
+  }
+
+  // slot_action(sc, r0, tile_start(n), repeat), branch-free.
+  TTCD_HD int act(int n, bool repeat) const {
+    const bool in1 = (n >= n1a) & (n <= n1b);
+    const bool in2 = (n >= n2a) & (n <= n2b);
+    const int normal = in1 ? ((in2 | ((dual != 0) & (n <= nl))) ? kStudentLast : kBand1)
+                           : (in2 ? kBand2 : kSkip);
+    return repeat ? ((in1 & in2) ? kFar : kSkip) : normal;
+  }
+  // !wave_full(r0, band of action a, tile_start(n)) for an action that is not kSkip.
+  TTCD_HD bool mask(int n, int a) const {
+    const bool far = (a == kBand2) | (a == kFar);
+    const int fa = far ? f2a : f1a, fz = far ? f2b : f1b;
+    return !((n >= fa) & (n <= fz));
+  }
+};
+
+// Query tokens swept by one workgroup (see Geometry; the same for every GQA group size).
+TTCD_HD int wg_span_tokens(int gqa_group) {
+  (void)gqa_group;
+  return kBlockM;
+}
 
 // Schedules built by the C ABI entry points (windows already validated).
 TTCD_HD Schedule make_dual_schedule(int T, int ws, int wt) {
