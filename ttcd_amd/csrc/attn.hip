@@ -51,6 +51,17 @@
 #include "internal.h"
 #include "schedule.h"
 
+// Software-pipeline depths of the slot body (see slot_body).
+#ifndef TTCD_R1
+#define TTCD_R1 3  // K operand reads in flight ahead of the score MFMAs
+#endif
+#ifndef TTCD_R2
+#define TTCD_R2 2  // V^T operands in flight ahead of the PV MFMAs
+#endif
+#ifndef TTCD_P1
+#define TTCD_P1 2  // score MFMAs issued before the reference max is settled
+#endif
+
 namespace ttcd {
 namespace {
 
@@ -354,9 +365,9 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
   using v8 = typename VecT<T>::v8;
   constexpr int N1 = 2 * G::DK;  // score MFMAs
   constexpr int N2 = 4 * G::DT;  // PV MFMAs
-  constexpr int R1 = 3;
-  constexpr int R2 = 2;
-  constexpr int P1 = 2;          // score MFMAs issued before settle()
+  constexpr int R1 = TTCD_R1;
+  constexpr int R2 = TTCD_R2;
+  constexpr int P1 = TTCD_P1;          // score MFMAs issued before settle()
   constexpr int H2 = N2 / 2;     // PV MFMAs carrying sums (the rest carry maxima)
   constexpr int A2 = 32 / H2;    // values summed / maxed per PV MFMA
 
@@ -472,7 +483,7 @@ void attn_fwd_kernel(AttnArgs a) {
   using v8 = typename VecT<T>::v8;
   __shared__ __attribute__((aligned(1024))) char smem_raw[G::NSTAGE * G::STAGE_B];
 
-  const int tid = threadIdx.x;
+  const int tid = __builtin_amdgcn_workitem_id_x();
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const Schedule sc = a.sched;
@@ -481,7 +492,7 @@ void attn_fwd_kernel(AttnArgs a) {
   // Workgroup -> (b, kv head, query block [heaviest first], head in group),
   // XCD-remapped: each XCD sweeps a contiguous run, so the query heads
   // sharing a K/V head and neighbouring query blocks share its L2.
-  int rest = xcd_remap(blockIdx.x, gridDim.x);
+  int rest = xcd_remap(__builtin_amdgcn_workgroup_id_x(), a.nwg);
   const int g = rest % a.G;
   rest /= a.G;
   const int qb = a.nqb - 1 - rest % a.nqb;
@@ -529,7 +540,7 @@ void attn_fwd_kernel(AttnArgs a) {
   const WaveSlots wsl(sc, r0);
   const int64_t kst = a.k_st, vst = a.v_st;
   // DMA of the K (or V) tile of tile index n into the K (V) half of stage s.
-  auto dma_half = [&](bool is_k, int n, int s) {
+  auto dma_half = [&](bool is_k, int n, int s) __attribute__((always_inline)) {
     const int j0 = sc.tile_start(n);
     const uint32_t dst = lds_base + s * G::STAGE_B + (is_k ? 0 : G::TILE_B);
     const T* base = is_k ? kp : vp;
@@ -601,7 +612,7 @@ void attn_fwd_kernel(AttnArgs a) {
   // slot runs the same code: a slot this wave skips folds all-zero
   // probabilities. Unrolled by two so the two score buffers swap roles
   // without register copies.
-  auto step = [&](f32x16 (&scur)[2], f32x16 (&snxt)[2], int k) {
+  auto step = [&](f32x16 (&scur)[2], f32x16 (&snxt)[2], int k) __attribute__((always_inline)) {
     const int n2 = walk.n;
     const bool rep2 = walk.rep;
     if (k + 2 < nslot) dma_half(true, n2, k & 1);
@@ -610,7 +621,7 @@ void attn_fwd_kernel(AttnArgs a) {
     // Mask S(k) if needed, then the reference max of slot k (lazy rescale):
     // moved, and O^T / l rescaled, only when some row's max exceeds it by
     // more than 2^kRescaleLog2. Returns m*c for the exp2 of slot k.
-    auto settle = [&]() {
+    auto settle = [&]() __attribute__((always_inline)) {
       float mx = mx_lane;
       if (__builtin_expect(cur.mask, 0)) {
         mask_band(scur, x.qrow, cur.j0, T_, cur.band, x.half);
@@ -636,7 +647,7 @@ void attn_fwd_kernel(AttnArgs a) {
       }
       return active ? ((m == -INFINITY) ? 0.f : m * x.c) : INFINITY;
     };
-    auto side = [&](int i) {
+    auto side = [&](int i) __attribute__((always_inline)) {
       if (i == 2) nxt = slot_info(sc, wsl, n1, rep1, wave_valid & (k + 1 < nslot));
     };
     mx_lane = slot_body<D, T>(x, scur, snxt, o, l, x.lds + ((k + 1) & 1) * G::STAGE_B,
@@ -676,8 +687,10 @@ void attn_fwd_kernel(AttnArgs a) {
 
 template <int D, typename T, bool DUAL>
 hipError_t launch_typed(const AttnArgs& a, hipStream_t stream) {
-  const int grid = a.B * a.Hq * a.nqb;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, T, DUAL>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
+  AttnArgs args = a;
+  args.nwg = a.B * a.Hq * a.nqb;
+  hipLaunchKernelGGL((attn_fwd_kernel<D, T, DUAL>), dim3(args.nwg), dim3(kWaves * 64), 0, stream,
+                     args);
   return hipGetLastError();
 }
 

@@ -25,6 +25,7 @@ struct AttnArgs {
   int64_t o_sb, o_st, o_sh;
   int B, T, Hq, Hkv, G;
   int nqb;        // query tiles of kBlockM tokens per (b, h)
+  int nwg;        // workgroups launched (set by the launcher)
   float c;        // sm_scale * log2(e)
   Schedule sched;
 };
