@@ -122,8 +122,9 @@ ttcd_status ttcd_causal_dwconv_chunked_fwd(const void* x, const void* w,
  * window_s <= i - j < window_t). Used by tests to prove every in-band pair
  * is visited exactly once. Set dual = 0 for the single-band schedule, in
  * which case window_s = band_lo and window_t = band_hi. gqa_group is the
- * query-head group size Hq/Hkv, which selects the workgroup geometry
- * (two heads x 128 tokens when even, one head x 256 tokens when odd).
+ * query-head group size Hq/Hkv (the current workgroup geometry, 128 tokens
+ * of one head, does not depend on it). Also checks the kernel's incremental
+ * slot walker and closed-form per-wave actions against the plan.
  */
 ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s,
                                         int window_t, int gqa_group,
