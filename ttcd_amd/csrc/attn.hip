@@ -426,9 +426,13 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
     if (i < H2) {
 #pragma unroll
       for (int j = 0; j < A2; j += 2) {
-        ps0 += score_at(sc, A2 * i + j);
-        ps1 += score_at(sc, A2 * i + j + 1);
+        const float a0 = score_at(sc, A2 * i + j), a1 = score_at(sc, A2 * i + j + 1);
+        ps0 = (i == 0 && j == 0) ? a0 : ps0 + a0;
+        ps1 = (i == 0 && j == 0) ? a1 : ps1 + a1;
       }
+      // pin the partial sums here: otherwise the chain is sunk to its use
+      // after the last MFMA, out of the MFMA shadow
+      asm volatile("" : "+v"(ps0), "+v"(ps1));
     } else {
 #pragma unroll
       for (int j = 0; j < A2; j += 4) {
@@ -436,13 +440,11 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
         mx0 = __builtin_fmaxf(__builtin_fmaxf(mx0, score_at(sn, idx)), score_at(sn, idx + 1));
         mx1 = __builtin_fmaxf(__builtin_fmaxf(mx1, score_at(sn, idx + 2)), score_at(sn, idx + 3));
       }
+      asm volatile("" : "+v"(mx0), "+v"(mx1));
     }
     if (i + R2 < N2) vt[i + R2] = read_vt<D, T>(vb[(i + R2) % G::DT], (i + R2) / G::DT);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // keep the sums in this block (the compiler would otherwise sink them to
-  // their use after the slot, out of the MFMA shadow)
-  asm volatile("" : "+v"(ps0), "+v"(ps1), "+v"(mx0), "+v"(mx1));
   l += ps0 + ps1;
   return fmaxf(mx0, mx1);
 }
