@@ -477,9 +477,20 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
   return reinterpret_cast<const T*>((uint64_t)lo | ((uint64_t)hi << 32));
 }
 
+// Wavefronts per SIMD: two for D = 128 (230 VGPRs); three for D = 64, whose
+// slots carry half the MFMA work for the same softmax VALU work and need
+// more waves to issue from (<= 168 VGPRs, 3 x 32 KiB of LDS per CU).
+#ifndef TTCD_D64_WAVES
+#define TTCD_D64_WAVES 3
+#endif
+template <int D>
+constexpr int waves_per_simd() {
+  return D == 64 ? TTCD_D64_WAVES : 2;
+}
+
 template <int D, typename T, bool DUAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(kWaves * 64, kWaves * 64),
-                          amdgpu_waves_per_eu(2, 2)))
+                          amdgpu_waves_per_eu(waves_per_simd<D>(), waves_per_simd<D>())))
 void attn_fwd_kernel(AttnArgs a) {
   using G = Geo<D>;
   using v8 = typename VecT<T>::v8;
