@@ -37,10 +37,12 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 
 CONFIGS = {
+    # rope_theta / qk_norm: configs/ipttcd/ipttcdv9_qwen3_0.6B_ct_64k_v2_swa8k.json:11,18 and
+    # configs/ipttcd/ipttcdv9_smollm2_360M_ct_64k_v2_swa8k.json:11,18
     "qwen3": dict(name="Qwen3-0.6B layer, 64K prefill", B=1, T=65536, Hq=16, Hkv=8, D=128,
-                  wt=8192, ws=4096),
+                  wt=8192, ws=4096, rope_theta=1e6, qk_norm=True),
     "smollm2": dict(name="SmolLM2-360M layer, 64K prefill", B=1, T=65536, Hq=15, Hkv=5, D=64,
-                    wt=8192, ws=4096),
+                    wt=8192, ws=4096, rope_theta=1e5, qk_norm=False),
 }
 
 
@@ -161,7 +163,18 @@ def profile_one(args) -> int:
     cfg = CONFIGS[args.config]
     B, T, H, HK, D, wt, ws = (cfg[k] for k in ("B", "T", "Hq", "Hkv", "D", "wt", "ws"))
     gen = torch.Generator(device=dev).manual_seed(0)
-    if args.only == "copy":
+    if args.only == "prologue":
+        q = torch.randn(B, T, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        k = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        from ttcd_amd import prologue
+        w = torch.ones(D, device=dev, dtype=torch.bfloat16)
+        cos, sin = prologue.rope_tables(prologue.rope_inv_freq(D, cfg["rope_theta"], dev), T)
+        norm = cfg["qk_norm"]
+        fn = lambda: prologue.qk_norm_rope(q, k, w if norm else None, w if norm else None,  # noqa: E731
+                                           1e-5, cos, sin)
+        from oracle import prologue_ref
+        work, unit = prologue_ref.prologue_bytes(B, T, H, HK, D), "GB/s"
+    elif args.only == "copy":
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
         fn, work, unit = (lambda: dst.copy_(src)), float(1 << 31), "GB/s"
@@ -188,6 +201,35 @@ def profile_one(args) -> int:
     return 0
 
 
+def prologue_measure(q, k, cfg) -> dict:
+    """The attention prologue (q/k RMSNorm + rotary, one pass) on the bench's own
+    q and k: HBM-bound, so GB/s against the 8 TB/s peak."""
+    import torch
+    from oracle import prologue_ref
+    from ttcd_amd import prologue
+
+    B, T, H, HK, D = q.shape[0], q.shape[1], q.shape[2], k.shape[2], q.shape[3]
+    dev = q.device
+    wq = (1.0 + 0.1 * torch.randn(D, device=dev, generator=torch.Generator(device=dev)
+                                  .manual_seed(1))).to(torch.bfloat16)
+    cos, sin = prologue.rope_tables(prologue.rope_inv_freq(D, cfg["rope_theta"], dev), T)
+    norm = cfg["qk_norm"]
+    fn = lambda: prologue.qk_norm_rope(q, k, wq if norm else None, wq if norm else None,  # noqa: E731
+                                       1e-5, cos, sin)
+    ms_p = time_gpu(fn, 20, 3)
+    nbytes = prologue_ref.prologue_bytes(B, T, H, HK, D)
+    gbps = nbytes / (ms_p * 1e-3) / 1e9
+    qk_bytes = B * T * (H + HK) * D * 2
+    table_bytes = 2 * T * (D // 2) * 2
+    # the reference's launches: q_norm, k_norm (each a read and a write), then
+    # rotary on q and on k (a read, a write and the table rows each)
+    ref_bytes = (2 * qk_bytes if norm else 0) + 2 * qk_bytes + 2 * table_bytes
+    return {"shape": {"B": B, "T": T, "Hq": H, "Hkv": HK, "D": D}, "qk_norm": norm,
+            "rope_theta": cfg["rope_theta"], "ms": ms_p, "GB_per_s": gbps,
+            "frac_of_hbm_peak": gbps / PEAK_HBM_GBPS, "algorithmic_bytes": nbytes,
+            "reference_launches_bytes": ref_bytes}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -198,7 +240,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-numerics", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", choices=["fused", "band", "lse", "conv", "copy"],
+    ap.add_argument("--only", choices=["fused", "band", "lse", "conv", "copy", "prologue"],
                     help="profiling mode: run one workload --steps times and print its timing")
     args = ap.parse_args()
 
@@ -263,6 +305,8 @@ def main() -> int:
                            "frac_of_hbm_peak": gbps / PEAK_HBM_GBPS,
                            "algorithmic_bytes": nbytes}
             del x, w
+            res["prologue"] = prologue_measure(q, k, cfg)
+            log(f"prologue (q/k RMSNorm + rotary): {res['prologue']}")
     if not args.no_numerics:
         res["numerics_config1"] = numerics_report()
         log(f"numerics: {res['numerics_config1']}")

@@ -114,6 +114,46 @@ ttcd_status ttcd_causal_dwconv_chunked_fwd(const void* x, const void* w,
                                            ttcd_dtype w_dtype, void* stream);
 
 /*
+ * Attention prologue: per-head RMSNorm of q and k (qk_norm) fused with the
+ * rotary embedding, one read and one write of q and k. Replaces, at
+ * profiling/patches.py:254-268, `q, k = attn.q_norm(q), attn.k_norm(k)`
+ * (fla RMSNorm forward, fla/modules/layernorm.py:189-251) followed by
+ * `q, k = attn.rotary(q, k, seqlen_offset=...)` (fla rotary_embedding_kernel,
+ * non-interleaved, fla/modules/rotary.py:43-135).
+ *
+ * q: (B, T, Hq, D), k: (B, T, Hkv, D) of `dtype` (BF16 or F16), D in {64, 128};
+ * q_out / k_out have the same shapes (they may alias q / k exactly).
+ * *_stride[4] = element strides of (b, t, h, d); d-stride 1.
+ * q_norm_w, k_norm_w: (D,) RMSNorm weights of w_dtype (BF16, F16 or F32), or
+ * both NULL for rotary only. Per row: var = sum(x^2) / D,
+ * y = (x / sqrt(var + eps)) * w rounded to dtype; then with x0 = y[:D/2],
+ * x1 = y[D/2:], c/s = the table rows at position t + seqlen_offset:
+ * out = [x0*c - x1*s, x0*s + x1*c] in fp32, rounded to dtype.
+ * cos_table, sin_table: (table_rows, D/2) contiguous, `dtype`;
+ * seqlen_offset + T <= table_rows.
+ */
+ttcd_status ttcd_qk_norm_rope_fwd(
+    const void* q, const void* k, void* q_out, void* k_out,
+    const void* q_norm_w, const void* k_norm_w, ttcd_dtype w_dtype, float eps,
+    const void* cos_table, const void* sin_table, int table_rows, int B, int T,
+    int Hq, int Hkv, int D, const int64_t q_stride[4],
+    const int64_t k_stride[4], const int64_t q_out_stride[4],
+    const int64_t k_out_stride[4], int seqlen_offset, ttcd_dtype dtype,
+    void* stream);
+
+/*
+ * Rotary tables as fla's RotaryEmbedding builds them
+ * (fla/modules/rotary.py:441-490, pos_idx_in_fp32): for t < rows and
+ * i < half_dim, cos_table[t*half_dim + i] = cos(fp32(t) * inv_freq[i]) and
+ * the same for sin, the product rounded once to fp32, the result rounded to
+ * `dtype` (BF16 or F16). inv_freq: half_dim fp32 values in device memory
+ * (the module's inv_freq buffer, rotary.py:418-425).
+ */
+ttcd_status ttcd_rope_table_fwd(void* cos_table, void* sin_table,
+                                const float* inv_freq, int rows, int half_dim,
+                                ttcd_dtype dtype, void* stream);
+
+/*
  * Host-only schedule check (no GPU work). Replays the attention kernels'
  * exact tile/phase schedule for one (b, h) slice of length T and adds, for
  * every (query i, key j) pair the kernel would fold into each output, one

@@ -33,6 +33,8 @@ EXPORTS = (
     "ttcd_band_attn_fwd",
     "ttcd_lse_merge_fwd",
     "ttcd_causal_dwconv_chunked_fwd",
+    "ttcd_qk_norm_rope_fwd",
+    "ttcd_rope_table_fwd",
     "ttcd_attn_schedule_coverage",
 )
 
@@ -61,6 +63,11 @@ _SIGS = {
         _i32, _i32, _i32, _i32, _i32, _i64x4, _i32, _vp]),
     "ttcd_causal_dwconv_chunked_fwd": (_i32, [
         _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "ttcd_qk_norm_rope_fwd": (_i32, [
+        _vp, _vp, _vp, _vp, _vp, _vp, _i32, ctypes.c_float,
+        _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
+        _i64x4, _i64x4, _i64x4, _i64x4, _i32, _i32, _vp]),
+    "ttcd_rope_table_fwd": (_i32, [_vp, _vp, _fp, _i32, _i32, _i32, _vp]),
     "ttcd_attn_schedule_coverage": (_i32, [
         _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
 }

@@ -209,6 +209,95 @@ ttcd_status ttcd_causal_dwconv_chunked_fwd(const void* x, const void* w, void* y
                   "depthwise conv launch");
 }
 
+ttcd_status ttcd_rope_table_fwd(void* cos_table, void* sin_table, const float* inv_freq,
+                                int rows, int half_dim, ttcd_dtype dtype, void* stream) {
+  if (!cos_table || !sin_table || !inv_freq)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (rows < 0 || half_dim < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need rows >= 0 and half_dim >= 1 (got %d, %d)", rows,
+                half_dim);
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "table dtype must be bf16 or f16");
+  if (rows == 0) return ok();
+  return from_hip(ttcd::launch_rope_table(cos_table, sin_table, inv_freq, rows, half_dim,
+                                          elem(dtype), static_cast<hipStream_t>(stream)),
+                  "rope table launch");
+}
+
+ttcd_status ttcd_qk_norm_rope_fwd(const void* q, const void* k, void* q_out, void* k_out,
+                                  const void* q_norm_w, const void* k_norm_w, ttcd_dtype w_dtype,
+                                  float eps, const void* cos_table, const void* sin_table,
+                                  int table_rows, int B, int T, int Hq, int Hkv, int D,
+                                  const int64_t q_stride[4], const int64_t k_stride[4],
+                                  const int64_t q_out_stride[4], const int64_t k_out_stride[4],
+                                  int seqlen_offset, ttcd_dtype dtype, void* stream) {
+  if (!q || !k || !q_out || !k_out || !cos_table || !sin_table)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null tensor pointer");
+  if (!q_stride || !k_stride || !q_out_stride || !k_out_stride)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null stride array");
+  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "give both norm weights or neither");
+  if (B < 1 || T < 1 || Hq < 1 || Hkv < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "B, T, Hq, Hkv must be >= 1 (got %d, %d, %d, %d)", B,
+                T, Hq, Hkv);
+  if (D != 64 && D != 128)
+    return fail(TTCD_ERR_UNSUPPORTED, "head_dim %d not supported (64 or 128)", D);
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "q/k dtype must be bf16 or f16");
+  if (q_norm_w && (unsigned)w_dtype > TTCD_DTYPE_F32)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "unknown norm weight dtype");
+  if (!(eps >= 0.f) || !isfinite(eps))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+  if (seqlen_offset < 0) return fail(TTCD_ERR_INVALID_ARGUMENT, "seqlen_offset must be >= 0");
+  if ((int64_t)seqlen_offset + T > (int64_t)table_rows)
+    return fail(TTCD_ERR_INVALID_ARGUMENT,
+                "rotary tables too short: seqlen_offset + T = %lld > table rows %d",
+                (long long)seqlen_offset + T, table_rows);
+  const int64_t* all[4] = {q_stride, k_stride, q_out_stride, k_out_stride};
+  for (int t = 0; t < 4; ++t) {
+    if (all[t][3] != 1)
+      return fail(TTCD_ERR_INVALID_ARGUMENT, "head_dim must be contiguous (d-stride 1)");
+    for (int i = 0; i < 3; ++i)
+      if (all[t][i] % 8 != 0 || all[t][i] < 0)
+        return fail(TTCD_ERR_UNSUPPORTED,
+                    "strides must be non-negative multiples of 8 elements (16-byte rows)");
+  }
+  if (!aligned16(q) || !aligned16(k) || !aligned16(q_out) || !aligned16(k_out) ||
+      !aligned16(cos_table) || !aligned16(sin_table))
+    return fail(TTCD_ERR_UNSUPPORTED, "tensor base pointers must be 16-byte aligned");
+  ttcd::PrologueArgs a = {};
+  a.q = q;
+  a.k = k;
+  a.q_out = q_out;
+  a.k_out = k_out;
+  a.q_w = q_norm_w;
+  a.k_w = k_norm_w;
+  a.cos = cos_table;
+  a.sin = sin_table;
+  a.eps = eps;
+  a.offset = seqlen_offset;
+  a.B = B;
+  a.T = T;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.D = D;
+  a.q_sb = q_stride[0];
+  a.q_st = q_stride[1];
+  a.q_sh = q_stride[2];
+  a.k_sb = k_stride[0];
+  a.k_st = k_stride[1];
+  a.k_sh = k_stride[2];
+  a.qo_sb = q_out_stride[0];
+  a.qo_st = q_out_stride[1];
+  a.qo_sh = q_out_stride[2];
+  a.ko_sb = k_out_stride[0];
+  a.ko_st = k_out_stride[1];
+  a.ko_sh = k_out_stride[2];
+  return from_hip(ttcd::launch_qk_norm_rope(a, elem(dtype), elem(w_dtype),
+                                            static_cast<hipStream_t>(stream)),
+                  "qk norm + rope launch");
+}
+
 ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int window_t,
                                         int gqa_group, int32_t* counts_near,
                                         int32_t* counts_far) {

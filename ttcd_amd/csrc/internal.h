@@ -1,5 +1,6 @@
 // internal.h - launcher interface between the C ABI (api.hip) and the
-// gfx950 kernels (attn.hip, conv.hip, merge.hip). Not part of the ABI.
+// gfx950 kernels (attn.hip, conv.hip, merge.hip, prologue.hip). Not part of
+// the ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -32,6 +33,31 @@ struct AttnArgs {
 
 // Launch the dual-window (sched.dual == 1) or single-band kernel.
 hipError_t launch_attn(const AttnArgs& a, int D, Elem dtype, hipStream_t stream);
+
+struct PrologueArgs {
+  const void* q;
+  const void* k;
+  void* q_out;
+  void* k_out;
+  const void* q_w;    // RMSNorm weights (both null: no norm)
+  const void* k_w;
+  const void* cos;    // (table_rows, D/2) contiguous, input dtype
+  const void* sin;
+  float eps;
+  int offset;         // position of token 0 in the tables
+  int B, T, Hq, Hkv, D;
+  int64_t q_sb, q_st, q_sh;
+  int64_t k_sb, k_st, k_sh;
+  int64_t qo_sb, qo_st, qo_sh;
+  int64_t ko_sb, ko_st, ko_sh;
+};
+
+// Fused q/k RMSNorm + rotary embedding (prologue.hip).
+hipError_t launch_qk_norm_rope(const PrologueArgs& a, Elem dtype, Elem wt, hipStream_t stream);
+
+// cos/sin tables: row t, column i = cos/sin(fp32(t) * inv_freq[i]) rounded to dtype.
+hipError_t launch_rope_table(void* cos_t, void* sin_t, const float* inv_freq, int rows, int half,
+                             Elem dtype, hipStream_t stream);
 
 hipError_t launch_dwconv(const void* x, const void* w, void* y, int64_t N, int C,
                          int D, int K, Elem xt, Elem wt, hipStream_t stream);
