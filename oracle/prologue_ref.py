@@ -20,16 +20,17 @@ the checker.
   rotate_complex_f64  the same rotation as complex multiplication
                       (x0 + i x1) * exp(i theta) in float64 (textbook form).
 
-Pins (tests/test_prologue.py): rope_ref == rotate_complex_f64 rounded once
-(each fp32 product of two 16-bit values is exact, so the only rounding is
-the final one); position 0 is the identity; rotating by a then b equals
-rotating by a + b in float64; norms are preserved; rms_norm_ref against a
-float64 evaluation within one rounding, closed forms (constant rows, zero
-rows, scale invariance); tables_ref against math.cos / math.sin.
+Pins (tests/test_prologue.py): rope_ref == rotate_complex_f64 rounded to
+fp32 and then to the dtype, bit for bit (each fp32 product of two 16-bit
+values is exact, so the fp32 expression is the exact value rounded once),
+and a planted sign / half swap fails that pin; position 0 is the identity;
+<rope(q, m), rope(k, n)> depends only on m - n; norms are preserved;
+rms_norm_ref within one rounding of a float64 evaluation, and closed forms
+(constant rows, zero rows, power-of-two scale invariance); inv_freq_ref
+against base ** (-2i / dim); tables_ref's column 0 (inv_freq 1) against
+math.cos / math.sin of the position.
 """
 from __future__ import annotations
-
-import math
 
 import torch
 
@@ -102,9 +103,3 @@ def prologue_bytes(B: int, T: int, Hq: int, Hkv: int, D: int, elem: int = 2) -> 
     """Algorithmic HBM bytes of one fused launch: q and k read once and written
     once (the cos/sin rows, T x D elements, are shared by every head)."""
     return 2 * B * T * (Hq + Hkv) * D * elem + 2 * T * (D // 2) * elem
-
-
-def angle_diff(a: float, b: float) -> float:
-    """|a - b| modulo 2 pi."""
-    d = math.fmod(abs(a - b), 2 * math.pi)
-    return min(d, 2 * math.pi - d)
