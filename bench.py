@@ -27,6 +27,7 @@ import platform
 import statistics
 import sys
 import time
+import types
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
@@ -37,12 +38,13 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 
 CONFIGS = {
-    # rope_theta / qk_norm: configs/ipttcd/ipttcdv9_qwen3_0.6B_ct_64k_v2_swa8k.json:11,18 and
-    # configs/ipttcd/ipttcdv9_smollm2_360M_ct_64k_v2_swa8k.json:11,18
+    # rope_theta / qk_norm / hidden / norm_eps:
+    # configs/ipttcd/ipttcdv9_qwen3_0.6B_ct_64k_v2_swa8k.json:3,11,14,18 and
+    # configs/ipttcd/ipttcdv9_smollm2_360M_ct_64k_v2_swa8k.json:3,11,14,18
     "qwen3": dict(name="Qwen3-0.6B layer, 64K prefill", B=1, T=65536, Hq=16, Hkv=8, D=128,
-                  wt=8192, ws=4096, rope_theta=1e6, qk_norm=True),
+                  wt=8192, ws=4096, rope_theta=1e6, qk_norm=True, hidden=1024, norm_eps=1e-6),
     "smollm2": dict(name="SmolLM2-360M layer, 64K prefill", B=1, T=65536, Hq=15, Hkv=5, D=64,
-                    wt=8192, ws=4096, rope_theta=1e5, qk_norm=False),
+                    wt=8192, ws=4096, rope_theta=1e5, qk_norm=False, hidden=960, norm_eps=1e-5),
 }
 
 
@@ -174,6 +176,15 @@ def profile_one(args) -> int:
                                            1e-5, cos, sin)
         from oracle import prologue_ref
         work, unit = prologue_ref.prologue_bytes(B, T, H, HK, D), "GB/s"
+    elif args.only == "epilogue":
+        from oracle import epilogue_ref
+        from ttcd_amd import epilogue
+        Hd = cfg["hidden"]
+        a_t, a_s, r = (torch.randn(B, T, Hd, device=dev, dtype=torch.bfloat16, generator=gen)
+                       for _ in range(3))
+        w = torch.ones(Hd, device=dev, dtype=torch.bfloat16)
+        fn = lambda: epilogue.dual_residual_rmsnorm(a_t, a_s, r, w, cfg["norm_eps"])  # noqa: E731
+        work, unit = epilogue_ref.epilogue_bytes(B * T, Hd), "GB/s"
     elif args.only == "copy":
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -230,6 +241,46 @@ def prologue_measure(q, k, cfg) -> dict:
             "reference_launches_bytes": ref_bytes}
 
 
+def epilogue_measure(o_t, o_s, cfg) -> dict:
+    """The attention epilogue on the fused kernel's outputs: the dual residual
+    RMSNorm alone (HBM-bound, GB/s against 8 TB/s), and the whole drop-in (one
+    o_proj GEMM over both outputs + the norm), with the stacked GEMM alone and
+    the reference's two GEMMs (one per output) timed beside it."""
+    import torch
+    import torch.nn.functional as F
+    from oracle import epilogue_ref
+    from ttcd_amd import epilogue
+
+    B, T = o_t.shape[0], o_t.shape[1]
+    Hd, eps = cfg["hidden"], cfg["norm_eps"]
+    dev = o_t.device
+    g = torch.Generator(device=dev).manual_seed(2)
+    r = torch.randn(B, T, Hd, device=dev, dtype=torch.bfloat16, generator=g)
+    a_t, a_s = (torch.randn(B, T, Hd, device=dev, dtype=torch.bfloat16, generator=g)
+                for _ in range(2))
+    w = (1.0 + 0.1 * torch.randn(Hd, device=dev, generator=g)).to(torch.bfloat16)
+    D_in = o_t.shape[2] * o_t.shape[3]
+    wo = (torch.randn(Hd, D_in, device=dev, generator=g) * D_in ** -0.5).to(torch.bfloat16)
+    o_proj = torch.nn.Linear(D_in, Hd, bias=False, device=dev, dtype=torch.bfloat16)
+    o_proj.weight.data.copy_(wo)
+    norm = types.SimpleNamespace(weight=w, bias=None, eps=eps)
+    ms_n = time_gpu(lambda: epilogue.dual_residual_rmsnorm(a_t, a_s, r, w, eps), 20, 3)
+    nbytes = epilogue_ref.epilogue_bytes(B * T, Hd)
+    gbps = nbytes / (ms_n * 1e-3) / 1e9
+    ms_f = time_gpu(lambda: epilogue.fused_attn_epilogue(o_proj, norm, o_t, o_s, r), 20, 3)
+    ot2, os2 = o_t.reshape(B, T, -1), o_s.reshape(B, T, -1)
+    ms_g2 = time_gpu(lambda: (F.linear(ot2, wo), F.linear(os2, wo)), 20, 3)
+    st = epilogue._stacked(ot2, os2)
+    ms_g1 = time_gpu(lambda: F.linear(st, wo), 20, 3)
+    # the reference's two fla launches: each reads attn and residual and writes
+    # y and the residual sum
+    ref_bytes = 2 * 4 * B * T * Hd * 2 + 2 * Hd * 2
+    return {"shape": {"rows": B * T, "hidden": Hd, "o_proj_in": D_in}, "norm_eps": eps,
+            "norm_ms": ms_n, "norm_GB_per_s": gbps, "norm_frac_of_hbm_peak": gbps / PEAK_HBM_GBPS,
+            "norm_algorithmic_bytes": nbytes, "reference_norm_launches_bytes": ref_bytes,
+            "drop_in_ms": ms_f, "stacked_gemm_ms": ms_g1, "two_gemms_ms": ms_g2}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,7 +291,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-numerics", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--only", choices=["fused", "band", "lse", "conv", "copy", "prologue"],
+    ap.add_argument("--only", choices=["fused", "band", "lse", "conv", "copy", "prologue",
+                                       "epilogue"],
                     help="profiling mode: run one workload --steps times and print its timing")
     args = ap.parse_args()
 
@@ -307,6 +359,10 @@ def main() -> int:
             del x, w
             res["prologue"] = prologue_measure(q, k, cfg)
             log(f"prologue (q/k RMSNorm + rotary): {res['prologue']}")
+            o_t, o_s = fused_dual_window_attn(q, k, v, wt, ws)
+            res["epilogue"] = epilogue_measure(o_t, o_s, cfg)
+            log(f"epilogue (o_proj + dual residual RMSNorm): {res['epilogue']}")
+            del o_t, o_s
     if not args.no_numerics:
         res["numerics_config1"] = numerics_report()
         log(f"numerics: {res['numerics_config1']}")

@@ -154,6 +154,25 @@ ttcd_status ttcd_rope_table_fwd(void* cos_table, void* sin_table,
                                 ttcd_dtype dtype, void* stream);
 
 /*
+ * Attention epilogue: the residual add + RMSNorm (prenorm) of the teacher and
+ * the student attention outputs in one pass. Replaces, at
+ * profiling/patches.py:296-298 (fuse_norm = True),
+ *   student_output, _ = mlp_norm(student_attn_output, residual, True)
+ *   hidden_states, residual = mlp_norm(teacher_attn_output, residual, True)
+ * (fla RMSNorm forward with a residual, fla/modules/layernorm.py:189-251,
+ * 715-764). All activations are (rows, hidden) contiguous of `dtype` (BF16 or
+ * F16); norm_w: (hidden,) of w_dtype (BF16, F16 or F32). Per row, for
+ * b in {t, s}: x_b = attn_b + residual in fp32, y_b = (x_b / sqrt(sum(x_b^2) /
+ * hidden + eps)) * w rounded to dtype; hidden_out = y_t, student_out = y_s,
+ * residual_out = x_t rounded to dtype. hidden % 8 == 0, hidden <= 2048.
+ */
+ttcd_status ttcd_dual_residual_rmsnorm_fwd(
+    const void* attn_t, const void* attn_s, const void* residual,
+    const void* norm_w, ttcd_dtype w_dtype, float eps, void* hidden_out,
+    void* residual_out, void* student_out, int64_t rows, int hidden,
+    ttcd_dtype dtype, void* stream);
+
+/*
  * Host-only schedule check (no GPU work). Replays the attention kernels'
  * exact tile/phase schedule for one (b, h) slice of length T and adds, for
  * every (query i, key j) pair the kernel would fold into each output, one

@@ -1,0 +1,143 @@
+"""Attention epilogue on the GPU (through the C ABI): the dual residual
+RMSNorm kernel against the CPU oracle, and the drop-in for the o_proj + norm
+call site against the reference's sequence of calls."""
+from __future__ import annotations
+
+import types
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attn_ref, epilogue_ref
+from ttcd_amd import attn, epilogue
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rand(shape, dtype=torch.bfloat16, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def _check(a_t, a_s, r, w, eps, y_t, res_out, y_s):
+    ry_t, rres, ry_s = epilogue_ref.dual_residual_rms_norm_ref(a_t, a_s, r, w, eps)
+    # the residual sum is one fp32 add of two 16-bit values: exact rounding
+    assert torch.equal(res_out.cpu(), rres)
+    # the norm differs from the oracle only in the order of the sum of squares
+    for got, want in ((y_t, ry_t), (y_s, ry_s)):
+        rep = attn_ref.ulp_report(got.cpu(), want)
+        assert rep["max_ulp"] <= 1 and rep["bit_equal_pct"] > 99.0, rep
+
+
+CASES = [
+    # B, T, H, dtype, w_dtype
+    pytest.param(1, 1000, 1024, torch.bfloat16, torch.bfloat16, id="qwen3-hidden"),
+    pytest.param(2, 333, 960, torch.bfloat16, torch.bfloat16, id="smollm2-360m-hidden"),
+    pytest.param(1, 257, 576, torch.bfloat16, torch.float32, id="smollm2-135m-f32w"),
+    pytest.param(1, 129, 2048, torch.float16, torch.float16, id="h2048-f16"),
+    pytest.param(3, 5, 8, torch.bfloat16, torch.bfloat16, id="h8"),
+    pytest.param(1, 1, 1024, torch.bfloat16, torch.bfloat16, id="one-row"),
+]
+
+
+@pytest.mark.parametrize("B,T,H,dtype,wdt", CASES)
+def test_matches_oracle(B, T, H, dtype, wdt):
+    a_t = _rand((B, T, H), dtype, 1)
+    a_s = _rand((B, T, H), dtype, 2)
+    r = _rand((B, T, H), dtype, 3, 4.0)
+    w = (1.0 + 0.2 * _rand((H,), torch.float32, 4)).to(wdt)
+    with torch.inference_mode():
+        out = epilogue.dual_residual_rmsnorm(a_t.to(DEV), a_s.to(DEV), r.to(DEV), w.to(DEV), 1e-6)
+    torch.cuda.synchronize()
+    _check(a_t, a_s, r, w, 1e-6, *out)
+
+
+def test_empty_rows():
+    x = torch.empty(1, 0, 1024, dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(1024, dtype=torch.bfloat16, device=DEV)
+    with torch.inference_mode():
+        y_t, res_out, y_s = epilogue.dual_residual_rmsnorm(x, x, x, w, 1e-6)
+    torch.cuda.synchronize()
+    assert y_t.shape == res_out.shape == y_s.shape == x.shape
+
+
+def _module_standins(H, D_in, seed):
+    o_proj = torch.nn.Linear(D_in, H, bias=False).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        o_proj.weight.copy_(_rand((H, D_in), seed=seed, scale=D_in ** -0.5))
+    norm = types.SimpleNamespace(
+        weight=(1.0 + 0.2 * _rand((H,), torch.float32, seed + 1)).to(DEV, torch.bfloat16),
+        bias=None, eps=1e-6)
+    return o_proj, norm
+
+
+def test_drop_in_matches_the_reference_sequence():
+    # profiling/patches.py:289-298: two o_proj GEMMs, then student and teacher
+    # residual RMSNorms. The fused path runs one GEMM over both outputs; a GEMM
+    # over 2x the rows may pick another kernel, so the projections agree to the
+    # GEMM's own rounding, and the norm on the fused projection is the oracle's
+    # (bitwise residual, 1 ulp outputs).
+    B, T, Hq, D, H = 1, 512, 16, 128, 1024
+    o_proj, norm = _module_standins(H, Hq * D, 11)
+    q = _rand((B, T, Hq, D), seed=12).to(DEV)
+    k = _rand((B, T, 8, D), seed=13).to(DEV)
+    v = _rand((B, T, 8, D), seed=14).to(DEV)
+    residual = _rand((B, T, H), seed=15, scale=4.0).to(DEV)
+    with torch.inference_mode():
+        o_t, o_s = attn.fused_dual_window_attn(q, k, v, 300, 100)
+        y_t, res_out, y_s = epilogue.fused_attn_epilogue(o_proj, norm, o_t, o_s, residual)
+        # the reference's sequence: separate GEMMs, then the two norms
+        a_t = F.linear(o_t.reshape(B, T, -1), o_proj.weight)
+        a_s = F.linear(o_s.reshape(B, T, -1), o_proj.weight)
+        proj = F.linear(torch.cat([o_t.reshape(B * T, -1), o_s.reshape(B * T, -1)]),
+                        o_proj.weight)
+    torch.cuda.synchronize()
+    for got, want in ((proj[:B * T], a_t.reshape(B * T, -1)),
+                      (proj[B * T:], a_s.reshape(B * T, -1))):
+        err = (got.float() - want.float()).abs().max().item()
+        assert err <= 2e-2 * max(1.0, want.float().abs().max().item()), err
+    _check(proj[:B * T].view(B, T, H).cpu(), proj[B * T:].view(B, T, H).cpu(), residual.cpu(),
+           norm.weight.cpu(), norm.eps, y_t, res_out, y_s)
+    ry_t, rres, ry_s = epilogue_ref.dual_residual_rms_norm_ref(
+        a_t.cpu(), a_s.cpu(), residual.cpu(), norm.weight.cpu(), norm.eps)
+    for got, want in ((y_t, ry_t), (y_s, ry_s), (res_out, rres)):
+        assert (got.cpu().float() - want.float()).abs().max().item() < 0.1
+
+
+def test_attention_outputs_are_halves_of_one_buffer():
+    # the stacked GEMM input is a view (no copy) for fused_dual_window_attn's outputs
+    B, T, Hq, D = 1, 64, 4, 64
+    q = _rand((B, T, Hq, D), seed=21).to(DEV)
+    k = _rand((B, T, 2, D), seed=22).to(DEV)
+    with torch.inference_mode():
+        o_t, o_s = attn.fused_dual_window_attn(q, k, k, 32, 16)
+        st = epilogue._stacked(o_t.reshape(B, T, -1), o_s.reshape(B, T, -1))
+    torch.cuda.synchronize()
+    assert st.data_ptr() == o_t.data_ptr() and st.shape == (2 * B * T, Hq * D)
+    assert torch.equal(st[:B * T], o_t.reshape(B * T, -1))
+    assert torch.equal(st[B * T:], o_s.reshape(B * T, -1))
+    # unrelated tensors are stacked by a copy
+    a, b = o_t.clone(), o_s.clone()
+    st2 = epilogue._stacked(a.reshape(B, T, -1), b.reshape(B, T, -1))
+    assert torch.equal(st2, st)
+
+
+def test_headline_shape():
+    # Qwen3-0.6B layer at 64K tokens: the residual sum on every row against
+    # torch's fp32 add, the norm on a strided sample of rows against the oracle
+    B, T, H = 1, 65536, 1024
+    g = torch.Generator(device=DEV).manual_seed(0)
+    a_t = torch.randn(B, T, H, device=DEV, dtype=torch.bfloat16, generator=g)
+    a_s = torch.randn(B, T, H, device=DEV, dtype=torch.bfloat16, generator=g)
+    r = (4 * torch.randn(B, T, H, device=DEV, generator=g)).to(torch.bfloat16)
+    w = (1.0 + 0.2 * torch.randn(H, device=DEV, generator=g)).to(torch.bfloat16)
+    with torch.inference_mode():
+        y_t, res_out, y_s = epilogue.dual_residual_rmsnorm(a_t, a_s, r, w, 1e-6)
+        want = (a_t.float() + r.float()).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(res_out, want)
+    rows = torch.arange(0, T, 37)
+    _check(a_t[:, rows].cpu(), a_s[:, rows].cpu(), r[:, rows].cpu(), w.cpu(), 1e-6,
+           y_t[:, rows], res_out[:, rows], y_s[:, rows])

@@ -10,16 +10,19 @@ bare-module drop-in used by patches.py):
     window_attn / band_attn / lse_merge
     qk_norm_rope / fused_qk_norm_rope / rope_tables / rope_inv_freq (attention
     prologue: q/k RMSNorm + rotary embedding in one pass)
+    dual_residual_rmsnorm / fused_attn_epilogue (attention epilogue: one o_proj
+    GEMM over both outputs, then both residual RMSNorms in one pass)
 """
 from .attn import (band_attn, fused_dual_window_attn, lse_dual_window_attn,
                    lse_dual_window_attn_fa3, lse_dual_window_attn_fa3_fast, lse_merge,
                    window_attn)
 from .conv import causal_dwconv_chunked, causal_dwconv_x
+from .epilogue import dual_residual_rmsnorm, fused_attn_epilogue
 from .prologue import fused_qk_norm_rope, qk_norm_rope, rope_inv_freq, rope_tables
 
 __all__ = [
     "band_attn", "causal_dwconv_chunked", "causal_dwconv_x", "fused_dual_window_attn",
     "lse_dual_window_attn", "lse_dual_window_attn_fa3", "lse_dual_window_attn_fa3_fast",
     "lse_merge", "window_attn", "fused_qk_norm_rope", "qk_norm_rope", "rope_inv_freq",
-    "rope_tables",
+    "rope_tables", "dual_residual_rmsnorm", "fused_attn_epilogue",
 ]

@@ -35,6 +35,7 @@ EXPORTS = (
     "ttcd_causal_dwconv_chunked_fwd",
     "ttcd_qk_norm_rope_fwd",
     "ttcd_rope_table_fwd",
+    "ttcd_dual_residual_rmsnorm_fwd",
     "ttcd_attn_schedule_coverage",
 )
 
@@ -68,6 +69,8 @@ _SIGS = {
         _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
         _i64x4, _i64x4, _i64x4, _i64x4, _i32, _i32, _vp]),
     "ttcd_rope_table_fwd": (_i32, [_vp, _vp, _fp, _i32, _i32, _i32, _vp]),
+    "ttcd_dual_residual_rmsnorm_fwd": (_i32, [
+        _vp, _vp, _vp, _vp, _i32, ctypes.c_float, _vp, _vp, _vp, _i64, _i32, _i32, _vp]),
     "ttcd_attn_schedule_coverage": (_i32, [
         _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
 }

@@ -81,8 +81,10 @@ def fused_dual_window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("block_n must be positive")
     B, T, H, HK, D = _check_qkv(q, k, v, "fused_dual_window_attn")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    ot = torch.empty_like(q)
-    os_ = torch.empty_like(q)
+    # o_t and o_s are the two contiguous halves of one allocation, so the
+    # epilogue can run one o_proj GEMM over both without a copy
+    both = torch.empty((2,) + tuple(q.shape), dtype=q.dtype, device=q.device)
+    ot, os_ = both[0], both[1]
     lse_t = lse_s = None
     if return_lse:
         lse_t = torch.empty(B, H, T, device=q.device, dtype=torch.float32)

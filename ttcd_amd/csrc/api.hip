@@ -298,6 +298,40 @@ ttcd_status ttcd_qk_norm_rope_fwd(const void* q, const void* k, void* q_out, voi
                   "qk norm + rope launch");
 }
 
+ttcd_status ttcd_dual_residual_rmsnorm_fwd(const void* attn_t, const void* attn_s,
+                                           const void* residual, const void* norm_w,
+                                           ttcd_dtype w_dtype, float eps, void* hidden_out,
+                                           void* residual_out, void* student_out,
+                                           int64_t rows, int hidden, ttcd_dtype dtype,
+                                           void* stream) {
+  if (!attn_t || !attn_s || !residual || !norm_w || !hidden_out || !residual_out ||
+      !student_out)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (rows < 0 || hidden < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need rows >= 0 and hidden >= 1");
+  if (hidden % 8 != 0 || hidden > 2048)
+    return fail(TTCD_ERR_UNSUPPORTED, "hidden size %d not supported (a multiple of 8, <= 2048)",
+                hidden);
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "activation dtype must be bf16 or f16");
+  if ((unsigned)w_dtype > TTCD_DTYPE_F32)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "unknown norm weight dtype");
+  if (!(eps >= 0.f) || !isfinite(eps))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+  const void* all[6] = {attn_t, attn_s, residual, hidden_out, residual_out, student_out};
+  for (int i = 0; i < 6; ++i)
+    if (!aligned16(all[i]))
+      return fail(TTCD_ERR_UNSUPPORTED, "tensor base pointers must be 16-byte aligned");
+  if (w_dtype != TTCD_DTYPE_F32 && !aligned16(norm_w))
+    return fail(TTCD_ERR_UNSUPPORTED, "16-bit norm weights must be 16-byte aligned");
+  if (rows == 0) return ok();
+  return from_hip(ttcd::launch_dual_residual_rmsnorm(
+                      attn_t, attn_s, residual, norm_w, elem(w_dtype), eps, hidden_out,
+                      residual_out, student_out, rows, hidden, elem(dtype),
+                      static_cast<hipStream_t>(stream)),
+                  "dual residual rmsnorm launch");
+}
+
 ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int window_t,
                                         int gqa_group, int32_t* counts_near,
                                         int32_t* counts_far) {

@@ -1,0 +1,161 @@
+// epilogue.hip - attention epilogue for gfx950: the residual add + RMSNorm of
+// the teacher and the student attention outputs in one pass.
+//
+// Replaces, at profiling/patches.py:296-298 (fuse_norm = True; the stock
+// forward has the same step at custom_models/ipttcd/modeling_ipttcdv9.py),
+//   student_output, _ = self.mlp_norm(student_attn_output, residual, True)
+//   hidden_states, residual = self.mlp_norm(teacher_attn_output, residual, True)
+// two launches of fla's RMSNorm forward with a residual and prenorm
+// (fla/modules/layernorm.py:189-251, 715-764), which read the residual twice
+// and also store the student's discarded residual sum. Per row of H values
+// and per branch b in {teacher, student}:
+//   x_b = f32(a_b) + f32(residual)           (one fp32 rounding)
+//   var_b = sum(x_b * x_b) / H,  rstd_b = 1 / sqrt(var_b + eps)
+//   y_b = (x_b * rstd_b) * w                  rounded to the dtype
+// and residual_out = x_teacher rounded to the dtype. The only freedom left is
+// the order of the sums of squares (lane-local in element order, then a
+// butterfly over the wavefront).
+//
+// One wavefront per row: lane l owns the 16-byte chunks l, l + 64, ... of
+// the row, so every access is a coalesced 1 KiB transaction.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "internal.h"
+
+namespace ttcd {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+union V8 {
+  u32x4 raw;
+  T e[8];
+};
+
+// Rounded to T as a separate step from the fp32 result (no fused
+// multiply-and-convert), as the reference stores an fp32 value.
+template <typename T>
+__device__ __forceinline__ T round_to(float v) {
+  asm volatile("" : "+v"(v));
+  return static_cast<T>(v);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// MAXC: 16-byte chunks per lane (H <= 512 * MAXC; the fp32 sums of both
+// branches stay in registers between the two passes, so H <= 2048).
+template <typename T, typename W, int MAXC>
+__global__ __launch_bounds__(256) void dual_residual_rmsnorm_kernel(
+    const T* __restrict__ a_t, const T* __restrict__ a_s, const T* __restrict__ res,
+    const W* __restrict__ w, float eps, T* __restrict__ y_t, T* __restrict__ res_out,
+    T* __restrict__ y_s, int64_t rows, int H) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / 64;
+  if (row >= rows) return;  // whole wavefront: rows are per wavefront
+  const int nch = H / 8;     // 16-byte chunks per row
+  const int64_t base = row * H;
+
+  float xt[MAXC][8], xs[MAXC][8];
+  float sst = 0.f, sss = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int ch = lane + 64 * c;
+    V8<T> vt, vs, vr;
+    vt.raw = vs.raw = vr.raw = u32x4{0u, 0u, 0u, 0u};
+    if (ch < nch) {
+      vt.raw = *reinterpret_cast<const u32x4*>(a_t + base + 8 * ch);
+      vs.raw = *reinterpret_cast<const u32x4*>(a_s + base + 8 * ch);
+      vr.raw = *reinterpret_cast<const u32x4*>(res + base + 8 * ch);
+    }
+    V8<T> ro;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float r = static_cast<float>(vr.e[e]);
+      xt[c][e] = static_cast<float>(vt.e[e]) + r;
+      xs[c][e] = static_cast<float>(vs.e[e]) + r;
+      ro.e[e] = round_to<T>(xt[c][e]);
+      sst = fmaf(xt[c][e], xt[c][e], sst);
+      sss = fmaf(xs[c][e], xs[c][e], sss);
+    }
+    if (ch < nch) *reinterpret_cast<u32x4*>(res_out + base + 8 * ch) = ro.raw;
+  }
+  sst = wave_sum(sst);
+  sss = wave_sum(sss);
+  const float rt = 1.0f / sqrtf(sst / (float)H + eps);
+  const float rs = 1.0f / sqrtf(sss / (float)H + eps);
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int ch = lane + 64 * c;
+    if (ch >= nch) break;
+    V8<W> vw[1];
+    float wf[8];
+    if (sizeof(W) == 2) {
+      vw[0].raw = *reinterpret_cast<const u32x4*>(w + 8 * ch);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wf[e] = static_cast<float>(vw[0].e[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wf[e] = static_cast<float>(w[8 * ch + e]);
+    }
+    V8<T> ot, os;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ot.e[e] = round_to<T>((xt[c][e] * rt) * wf[e]);
+      os.e[e] = round_to<T>((xs[c][e] * rs) * wf[e]);
+    }
+    *reinterpret_cast<u32x4*>(y_t + base + 8 * ch) = ot.raw;
+    *reinterpret_cast<u32x4*>(y_s + base + 8 * ch) = os.raw;
+  }
+}
+
+template <typename T, typename W, int MAXC>
+hipError_t launch_c(const void* a_t, const void* a_s, const void* res, const void* w, float eps,
+                    void* y_t, void* res_out, void* y_s, int64_t rows, int H, hipStream_t st) {
+  const int64_t blocks = (rows + 3) / 4;
+  hipLaunchKernelGGL((dual_residual_rmsnorm_kernel<T, W, MAXC>), dim3((unsigned)blocks),
+                     dim3(256), 0, st, static_cast<const T*>(a_t), static_cast<const T*>(a_s),
+                     static_cast<const T*>(res), static_cast<const W*>(w), eps,
+                     static_cast<T*>(y_t), static_cast<T*>(res_out), static_cast<T*>(y_s), rows,
+                     H);
+  return hipGetLastError();
+}
+
+template <typename T, typename W>
+hipError_t launch_h(const void* a_t, const void* a_s, const void* res, const void* w, float eps,
+                    void* y_t, void* res_out, void* y_s, int64_t rows, int H, hipStream_t st) {
+  const int nch = H / 8;
+  if (nch <= 64) return launch_c<T, W, 1>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
+  if (nch <= 128) return launch_c<T, W, 2>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
+  return launch_c<T, W, 4>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
+}
+
+template <typename T>
+hipError_t launch_w(const void* a_t, const void* a_s, const void* res, const void* w, Elem wt,
+                    float eps, void* y_t, void* res_out, void* y_s, int64_t rows, int H,
+                    hipStream_t st) {
+  switch (wt) {
+    case Elem::BF16: return launch_h<T, __bf16>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
+    case Elem::F16: return launch_h<T, _Float16>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
+    default: return launch_h<T, float>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_dual_residual_rmsnorm(const void* a_t, const void* a_s, const void* res,
+                                        const void* w, Elem wt, float eps, void* y_t,
+                                        void* res_out, void* y_s, int64_t rows, int H,
+                                        Elem dtype, hipStream_t stream) {
+  return dtype == Elem::BF16
+             ? launch_w<__bf16>(a_t, a_s, res, w, wt, eps, y_t, res_out, y_s, rows, H, stream)
+             : launch_w<_Float16>(a_t, a_s, res, w, wt, eps, y_t, res_out, y_s, rows, H, stream);
+}
+
+}  // namespace ttcd

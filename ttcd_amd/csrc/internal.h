@@ -1,6 +1,6 @@
 // internal.h - launcher interface between the C ABI (api.hip) and the
-// gfx950 kernels (attn.hip, conv.hip, merge.hip, prologue.hip). Not part of
-// the ABI.
+// gfx950 kernels (attn.hip, conv.hip, merge.hip, prologue.hip, epilogue.hip).
+// Not part of the ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -58,6 +58,12 @@ hipError_t launch_qk_norm_rope(const PrologueArgs& a, Elem dtype, Elem wt, hipSt
 // cos/sin tables: row t, column i = cos/sin(fp32(t) * inv_freq[i]) rounded to dtype.
 hipError_t launch_rope_table(void* cos_t, void* sin_t, const float* inv_freq, int rows, int half,
                              Elem dtype, hipStream_t stream);
+
+// Teacher and student residual add + RMSNorm of the attention outputs (epilogue.hip).
+hipError_t launch_dual_residual_rmsnorm(const void* a_t, const void* a_s, const void* res,
+                                        const void* w, Elem wt, float eps, void* y_t,
+                                        void* res_out, void* y_s, int64_t rows, int H,
+                                        Elem dtype, hipStream_t stream);
 
 hipError_t launch_dwconv(const void* x, const void* w, void* y, int64_t N, int C,
                          int D, int K, Elem xt, Elem wt, hipStream_t stream);
