@@ -14,7 +14,9 @@ Prints progress on stderr and ONE JSON line on stdout. Beside the headline
 it reports: the "two separate windowed calls" comparator (the single-band
 kernel at w_T then w_S), one teacher-only call, the LSE-combination variant,
 the chunked causal conv at the reference's benchmark shape (GB/s vs 8 TB/s),
-numerics at the CPU-runnable config, and the CPU baseline: the fp32 masked
+the attention prologue (q/k RMSNorm + rotary) and epilogue (o_proj + dual
+residual RMSNorm) on the same layer, the batch / narrow-gap sweep (fused vs
+LSE variant), numerics at the CPU-runnable config, and the CPU baseline: the fp32 masked
 softmax of the reference's CPU path (oracle restatement), query-chunked over
 the band, on a bounded sample of rows, on this host's cores.
 """
@@ -241,6 +243,45 @@ def prologue_measure(q, k, cfg) -> dict:
             "reference_launches_bytes": ref_bytes}
 
 
+SWEEP = [
+    # the batch and narrow-gap sweep at the Qwen3-0.6B head shape (Hq=16, Hkv=8, D=128)
+    dict(B=1, T=16384, wt=8192, ws=4096), dict(B=2, T=16384, wt=8192, ws=4096),
+    dict(B=4, T=16384, wt=8192, ws=4096), dict(B=8, T=16384, wt=8192, ws=4096),
+    dict(B=1, T=32768, wt=8192, ws=7168), dict(B=1, T=32768, wt=8192, ws=8064),
+]
+
+
+def sweep_measure(steps: int = 10, warmup: int = 2) -> list:
+    """Fused one-pass kernel (with both LSEs, as the headline) against the
+    LSE-combination variant at each sweep point; TFLOP/s over the teacher
+    band F = 4*B*Hq*D*P(T, w_T) for both."""
+    import torch
+    from oracle import attn_ref
+    from ttcd_amd import fused_dual_window_attn, lse_dual_window_attn
+
+    dev = torch.device("cuda:0")
+    H, HK, D = 16, 8, 128
+    out = []
+    for pt in SWEEP:
+        B, T, wt, ws = pt["B"], pt["T"], pt["wt"], pt["ws"]
+        gen = torch.Generator(device=dev).manual_seed(0)
+        q = torch.randn(B, T, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        k = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        v = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
+        F = attn_ref.attn_flops(B, H, D, T, wt)
+        ms_f = time_gpu(lambda: fused_dual_window_attn(q, k, v, wt, ws, return_lse=True),
+                        steps, warmup)
+        ms_l = time_gpu(lambda: lse_dual_window_attn(q, k, v, wt, ws), steps, warmup)
+        tf, tl = F / (ms_f * 1e-3) / 1e12, F / (ms_l * 1e-3) / 1e12
+        out.append({**pt, "Hq": H, "Hkv": HK, "D": D, "flops": F, "fused_ms": ms_f,
+                    "fused_tflops": tf, "fused_frac": tf / PEAK_BF16_TFLOPS, "lse_ms": ms_l,
+                    "lse_tflops": tl, "fused_speedup_vs_lse": ms_l / ms_f})
+        log(f"sweep B={B} T={T} ({wt},{ws}): fused {ms_f:.3f} ms {tf:.0f} TF/s, "
+            f"LSE {ms_l:.3f} ms {tl:.0f} TF/s")
+        del q, k, v
+    return out
+
+
 def epilogue_measure(o_t, o_s, cfg) -> dict:
     """The attention epilogue on the fused kernel's outputs: the dual residual
     RMSNorm alone (HBM-bound, GB/s against 8 TB/s), and the whole drop-in (one
@@ -292,7 +333,7 @@ def main() -> int:
     ap.add_argument("--no-numerics", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--only", choices=["fused", "band", "lse", "conv", "copy", "prologue",
-                                       "epilogue"],
+                                       "epilogue", "sweep"],
                     help="profiling mode: run one workload --steps times and print its timing")
     args = ap.parse_args()
 
@@ -306,6 +347,11 @@ def main() -> int:
     from ttcd_amd import (causal_dwconv_x, fused_dual_window_attn, lse_dual_window_attn,
                           window_attn)
 
+    if args.only == "sweep":
+        with torch.inference_mode():
+            print(json.dumps({"only": "sweep", "points": sweep_measure(args.steps, args.warmup)}),
+                  flush=True)
+        return 0
     if args.only:
         return profile_one(args)
 
@@ -363,6 +409,7 @@ def main() -> int:
             res["epilogue"] = epilogue_measure(o_t, o_s, cfg)
             log(f"epilogue (o_proj + dual residual RMSNorm): {res['epilogue']}")
             del o_t, o_s
+            res["config4_sweep"] = sweep_measure()
     if not args.no_numerics:
         res["numerics_config1"] = numerics_report()
         log(f"numerics: {res['numerics_config1']}")
