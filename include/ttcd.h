@@ -173,6 +173,59 @@ ttcd_status ttcd_dual_residual_rmsnorm_fwd(
     ttcd_dtype dtype, void* stream);
 
 /*
+ * One RMSNorm over rows of `hidden` elements, in one of fla's two forward
+ * forms (fla/modules/layernorm.py:189-251, 715-764):
+ *   residual == NULL: y = RMSNorm(x) * w (plain; attn_norm at
+ *     custom_models/ipttcd/modeling_ipttcdv9.py:627 and the final norm at
+ *     :1112);
+ *   residual != NULL: the prenorm form of :863, x' = f32(x) + f32(residual),
+ *     residual_out = x' rounded, y = RMSNorm(x') * w with the variance of the
+ *     unrounded x'.
+ * Pass residual and residual_out both or neither. Numerics, layout and
+ * limits as ttcd_dual_residual_rmsnorm_fwd.
+ */
+ttcd_status ttcd_rmsnorm_fwd(const void* x, const void* residual,
+                             const void* norm_w, ttcd_dtype w_dtype, float eps,
+                             void* y, void* residual_out, int64_t rows,
+                             int hidden, ttcd_dtype dtype, void* stream);
+
+/*
+ * SwiGLU, fla's swiglu_fwd (fla/modules/activations.py:412-471, used by
+ * swiglu and swiglu_linear in every MLP of the model): out = (g * s) * u
+ * with s = 1 / (1 + exp(-g)), in fp32, rounded to dtype. Row-strided
+ * (strides in elements, multiples of 8; cols % 8 == 0), so gate and up may
+ * be the two halves of one (rows, 2*cols) GEMM output.
+ */
+ttcd_status ttcd_swiglu_fwd(const void* gate, const void* up, void* out,
+                            int64_t rows, int cols, int64_t gate_stride,
+                            int64_t up_stride, int64_t out_stride,
+                            ttcd_dtype dtype, void* stream);
+
+/*
+ * The TTT MLP's feature pass in one launch. Replaces, in the TTT MLP's
+ * forward (custom_models/ipttcd/modeling_ipttcdv9_lowcopy_scanfuse.py:48-70,
+ * with the chunk-local conv of profiling/patches.py:411-432, and the diff of
+ * the update loop at :117-120), the launches
+ *   z = swiglu(gate_t, up_t); z_hat = swiglu(gate_s, up_s);
+ *   z_target = conv_t(z); z_hat = conv_s(z_hat); diff = z_target - z_hat.
+ * gu_t / gu_s: (B * nchunk * chunk, 2 * inter) teacher / student gate|up
+ * rows (gate in columns [0, inter), up in [inter, 2 * inter)), row stride
+ * gu_stride elements. conv_t / conv_s: (inter, kernel_size) depthwise causal
+ * conv weights, chunk-local (zero history at each chunk start), or NULL for
+ * no conv. Outputs (contiguous): z (rows, inter), z_hat (rows, inter) and
+ * diff (B * (nchunk - 1) * chunk, inter) for every chunk but the last of each
+ * batch row (NULL allowed when nchunk == 1). Every value is rounded to dtype
+ * where the reference stores it; the convs accumulate in fp32 in tap order.
+ * inter % 8 == 0, kernel_size <= 8.
+ */
+ttcd_status ttcd_ttt_features_fwd(const void* gu_t, const void* gu_s,
+                                  int64_t gu_stride, const void* conv_t,
+                                  const void* conv_s, ttcd_dtype w_dtype,
+                                  int kernel_size, void* z, void* z_hat,
+                                  void* diff, int B, int nchunk, int chunk,
+                                  int inter, ttcd_dtype dtype, void* stream);
+
+/*
  * Host-only schedule check (no GPU work). Replays the attention kernels'
  * exact tile/phase schedule for one (b, h) slice of length T and adds, for
  * every (query i, key j) pair the kernel would fold into each output, one

@@ -1,0 +1,181 @@
+"""ipttcdv9 prefill on the GPU: the new kernels (RMSNorm, SwiGLU, the TTT
+feature pass) through the C ABI against the CPU oracle, the TTT MLP against
+the oracle's group loop, and the whole model's logits against the oracle's
+prefill on a small config."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import attn_ref, epilogue_ref, ipttcdv9_ref as R, prologue_ref
+from ttcd_amd import epilogue, ipttcdv9 as M, ttt
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rand(*shape, seed=0, scale=1.0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def _ulp_ok(got, want, pct=99.0, max_ulp=1):
+    rep = attn_ref.ulp_report(got.cpu(), want.cpu())
+    assert rep["max_ulp"] <= max_ulp and rep["bit_equal_pct"] > pct, rep
+
+
+# ------------------------------------------------------------------ kernels
+
+
+@pytest.mark.parametrize("H,res,wdt", [(1024, False, torch.bfloat16), (1024, True, torch.bfloat16),
+                                       (960, True, torch.float32), (64, False, torch.float16)])
+def test_rmsnorm_matches_oracle(H, res, wdt):
+    dt = torch.float16 if wdt == torch.float16 else torch.bfloat16
+    x = _rand(3, 101, H, seed=1, dtype=dt)
+    r = _rand(3, 101, H, seed=2, scale=3.0, dtype=dt)
+    w = (1 + 0.2 * _rand(H, seed=3, dtype=torch.float32)).to(wdt)
+    with torch.inference_mode():
+        out = epilogue.rmsnorm(x.to(DEV), w.to(DEV), 1e-6, residual=r.to(DEV) if res else None)
+    torch.cuda.synchronize()
+    if res:
+        y, ro = out
+        ry, rro = epilogue_ref.residual_rms_norm_ref(x, r, w, 1e-6)
+        assert torch.equal(ro.cpu(), rro)
+    else:
+        y, ry = out, prologue_ref.rms_norm_ref(x, w, 1e-6)
+    _ulp_ok(y, ry)
+
+
+def test_swiglu_matches_oracle_on_strided_halves():
+    gu = _rand(777, 2 * 3072, seed=4, scale=2.0)
+    with torch.inference_mode():
+        g = gu.to(DEV)
+        z = ttt.swiglu(g[:, :3072], g[:, 3072:])
+    torch.cuda.synchronize()
+    _ulp_ok(z, R.swiglu_ref(gu[:, :3072], gu[:, 3072:]), pct=99.9)
+
+
+FEAT = [
+    # B, nchunk, C, I, K, conv_t, conv_s, w dtype
+    pytest.param(1, 4, 256, 512, 5, True, True, torch.bfloat16, id="both-convs"),
+    pytest.param(2, 3, 40, 64, 3, True, False, torch.float32, id="ragged-run-teacher-only-f32w"),
+    pytest.param(1, 2, 64, 128, 5, False, True, torch.bfloat16, id="student-only"),
+    pytest.param(1, 1, 96, 64, 5, True, True, torch.bfloat16, id="one-chunk"),
+    pytest.param(1, 3, 32, 64, 1, False, False, torch.bfloat16, id="no-conv"),
+]
+
+
+@pytest.mark.parametrize("B,nchunk,C,I,K,ct,cs,wdt", FEAT)
+def test_ttt_features_bitwise_chain(B, nchunk, C, I, K, ct, cs, wdt):
+    """z within one rounding of the oracle's swiglu; z_hat and diff bit for bit
+    equal to the oracle's conv and subtraction of the kernel's own swiglu
+    values (a second call with the student rows on both sides yields them)."""
+    rows = B * nchunk * C
+    gu_t = _rand(rows, 2 * I, seed=5, scale=2.0)
+    gu_s = _rand(rows, 2 * I, seed=6, scale=2.0)
+    w_t = _rand(I, 1, K, seed=7, scale=0.5, dtype=wdt) if ct else None
+    w_s = _rand(I, 1, K, seed=8, scale=0.5, dtype=wdt) if cs else None
+    d = lambda v: None if v is None else v.to(DEV)  # noqa: E731
+    with torch.inference_mode():
+        z, zh, diff = ttt.ttt_features(gu_t.to(DEV), gu_s.to(DEV), d(w_t), d(w_s), B, nchunk, C)
+        zr, _, _ = ttt.ttt_features(gu_s.to(DEV), gu_s.to(DEV), None, None, B, nchunk, C)
+    torch.cuda.synchronize()
+    _ulp_ok(z, R.swiglu_ref(gu_t[:, :I], gu_t[:, I:]), pct=99.9)
+    z4, zr4 = z.cpu().reshape(B, nchunk, C, I), zr.cpu().reshape(B, nchunk, C, I)
+    want_zh = R.conv_chunks(zr4, w_s).reshape(-1, I)
+    assert torch.equal(zh.cpu(), want_zh)
+    tgt = R.conv_chunks(z4, w_t)
+    want_diff = (tgt[:, :nchunk - 1].float() - want_zh.reshape(B, nchunk, C, I)[:, :nchunk - 1]
+                 .float()).to(z.dtype).reshape(-1, I)
+    assert diff.shape == want_diff.shape and torch.equal(diff.cpu(), want_diff)
+
+
+# ------------------------------------------------------------------ TTT MLP
+
+
+def _ttt_setup(B, L, H, I, K, seed=0):
+    g = torch.Generator().manual_seed(seed)
+
+    def n(*s, std):
+        return (torch.randn(*s, generator=g) * std).to(torch.bfloat16)
+    w = ttt.TttMlpWeights(n(2 * I, H, std=H ** -0.5).to(DEV), n(H, I, std=I ** -0.5).to(DEV),
+                          n(H, H, std=H ** -0.5).to(DEV), n(I, 1, K, std=0.4).to(DEV),
+                          n(I, 1, K, std=0.4).to(DEV), n(H, std=H ** -0.5).to(DEV))
+    x, t = n(B, L, H, std=1.0).to(DEV), n(B, L, H, std=1.0).to(DEV)
+    return w, x, t
+
+
+@pytest.mark.parametrize("B,L,C,G", [(1, 1024, 256, 16), (2, 700, 128, 2), (1, 256, 256, 4)])
+def test_ttt_mlp_matches_oracle_loop(B, L, C, G):
+    H, I, K = 256, 512, 5
+    w, x, t = _ttt_setup(B, L, H, I, K, seed=B + L)
+    with torch.inference_mode():
+        y = ttt.ttt_mlp(x, t, w, chunk=C, lr=0.3, update_every=G)
+        y2 = ttt.ttt_mlp(x, t, w, chunk=C, lr=0.3, update_every=G, fused=False)
+        # the oracle loop on the kernel's own features (same padding as the model)
+        nch = -(-L // C)
+        pad = nch * C - L
+        xp = torch.nn.functional.pad(x, (0, 0, 0, pad))
+        tp = torch.nn.functional.pad(t, (0, 0, 0, pad))
+        gu = torch.nn.functional.linear(torch.cat([xp.reshape(-1, H), tp.reshape(-1, H)]),
+                                        w.gate_up)
+        rows = B * nch * C
+        z, zh, diff = ttt.ttt_features(gu[:rows], gu[rows:], w.conv_t, w.conv_s, B, nch, C)
+    torch.cuda.synchronize()
+    # fused and separate feature passes are the same values, so the same output
+    assert torch.equal(y, y2)
+    cpu = lambda v: v.cpu()  # noqa: E731
+    want = R.ttt_mlp_scan_ref(cpu(z), cpu(zh), cpu(diff), cpu(tp), cpu(w.down), cpu(w.ttt_proj),
+                              cpu(w.b_proj), lr=0.3, update_every=G, B=B, nchunk=nch, C=C)[:, :L]
+    plain = (z.cpu().float() @ w.down.cpu().float().t()).reshape(B, nch * C, H)[:, :L]
+    yf, wf = y.cpu().float(), want.float()
+    rel = (yf - wf).norm() / wf.norm()
+    assert rel < 1e-2, rel
+    assert (yf - wf).abs().max() <= 3e-2 * wf.abs().max()
+    if nch > 1:  # the update path is exercised: the output is not the plain MLP's
+        assert (wf - plain).norm() / wf.norm() > 0.05
+
+
+# -------------------------------------------------------------------- model
+
+TINY = dict(M.QWEN3_06B_SWA8K, hidden_size=256, num_hidden_layers=3, num_heads=4, num_kv_heads=2,
+            head_dim=128, intermediate_size=512, vocab_size=1024, window_size=512,
+            ttt_layers=[0, 2], ttt_chunk=256, ttt_update_every=2,
+            ttt_teacher_conv_init="random", ttt_student_conv_init="random",
+            max_position_embeddings=1024)
+
+
+def _logits_close(got, want, max_frac=3e-2, mean_frac=2e-2):
+    g, w = got.float().cpu(), want.float().cpu()
+    d = (g - w).abs()
+    assert d.max() <= max_frac * w.abs().max(), (d.max(), w.abs().max())
+    assert d.mean() <= mean_frac * w.abs().mean(), (d.mean(), w.abs().mean())
+
+
+@pytest.mark.parametrize("T", [1024, 900, 200])
+def test_prefill_matches_oracle(T):
+    """T=1024: 4 chunks in 2 update groups; T=900: a zero-padded last chunk;
+    T=200: shorter than a chunk, so the TTT layers take the plain path."""
+    c = M.resolve_config(TINY)
+    w = M.init_weights(TINY, DEV, seed=0)
+    model = M.IPTTCDv9Prefill(TINY, w)
+    ids = torch.randint(0, c["vocab_size"], (1, T), generator=torch.Generator().manual_seed(T))
+    got = model.forward(ids.to(DEV), logits_to_keep=8)
+    got2 = model.forward(ids.to(DEV), logits_to_keep=8, fused=False)
+    torch.cuda.synchronize()
+    want = R.prefill_ref(c, {k: v.cpu() for k, v in w.items()}, ids, 8, torch.bfloat16)
+    _logits_close(got, want)
+    _logits_close(got2, want)
+    # the fused kernels change only rounding
+    _logits_close(got, got2, max_frac=2e-2, mean_frac=1e-2)
+
+
+def test_prefill_batch_rows_are_independent():
+    c = M.resolve_config(TINY)
+    w = M.init_weights(TINY, DEV, seed=1)
+    model = M.IPTTCDv9Prefill(TINY, w)
+    ids = torch.randint(0, c["vocab_size"], (2, 512), generator=torch.Generator().manual_seed(9))
+    both = model.forward(ids.to(DEV), logits_to_keep=4)
+    one = model.forward(ids[1:].to(DEV), logits_to_keep=4)
+    torch.cuda.synchronize()
+    _logits_close(both[1:], one, max_frac=1e-2, mean_frac=5e-3)

@@ -54,6 +54,16 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, fn: str):
     return B, T, H, HK, D
 
 
+def _ready(t: torch.Tensor) -> torch.Tensor:
+    """t itself when the C ABI takes it as is (unit head_dim stride, element
+    strides multiples of 8, 16-byte aligned base), else a contiguous copy: a
+    q / k / v view of one fused projection output needs no copy."""
+    if (t.stride(-1) == 1 and all(st % 8 == 0 for st in t.stride()[:-1])
+            and t.data_ptr() % 16 == 0):
+        return t
+    return t.contiguous()
+
+
 def _lse_ptr(t):
     return None if t is None else t.data_ptr()
 
@@ -80,10 +90,10 @@ def fused_dual_window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if int(block_n) <= 0:
         raise ValueError("block_n must be positive")
     B, T, H, HK, D = _check_qkv(q, k, v, "fused_dual_window_attn")
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    q, k, v = _ready(q), _ready(k), _ready(v)
     # o_t and o_s are the two contiguous halves of one allocation, so the
     # epilogue can run one o_proj GEMM over both without a copy
-    both = torch.empty((2,) + tuple(q.shape), dtype=q.dtype, device=q.device)
+    both = torch.empty((2,) + tuple(q.shape), dtype=q.dtype, device=q.device)  # contiguous
     ot, os_ = both[0], both[1]
     lse_t = lse_s = None
     if return_lse:
@@ -114,8 +124,8 @@ def band_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, band_lo: int, b
         band_hi = max(T, band_lo + 1)
     if not (0 <= band_lo < band_hi):
         raise ValueError(f"band_attn: need 0 <= band_lo < band_hi, got ({band_lo}, {band_hi})")
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    o = torch.empty_like(q)
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, T, device=q.device, dtype=torch.float32) if return_lse else None
     L = _lib.lib()
     _lib.check(L.ttcd_band_attn_fwd(

@@ -24,7 +24,7 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libttcd_amd.so")
 
-SOURCES = ["attn.hip", "conv.hip", "merge.hip", "prologue.hip", "epilogue.hip", "api.hip"]
+SOURCES = ["attn.hip", "conv.hip", "merge.hip", "prologue.hip", "epilogue.hip", "ttt.hip", "api.hip"]
 # attn.hip has no NaN-dependent logic; without IEEE mode max/min of MFMA
 # results need no canonicalising moves.
 SOURCE_FLAGS = {"attn.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}

@@ -332,6 +332,85 @@ ttcd_status ttcd_dual_residual_rmsnorm_fwd(const void* attn_t, const void* attn_
                   "dual residual rmsnorm launch");
 }
 
+ttcd_status ttcd_rmsnorm_fwd(const void* x, const void* residual, const void* norm_w,
+                             ttcd_dtype w_dtype, float eps, void* y, void* residual_out,
+                             int64_t rows, int hidden, ttcd_dtype dtype, void* stream) {
+  if (!x || !norm_w || !y) return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if ((residual == nullptr) != (residual_out == nullptr))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "pass residual and residual_out both or neither");
+  if (rows < 0 || hidden < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need rows >= 0 and hidden >= 1");
+  if (hidden % 8 != 0 || hidden > 2048)
+    return fail(TTCD_ERR_UNSUPPORTED, "hidden size %d not supported (a multiple of 8, <= 2048)",
+                hidden);
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "activation dtype must be bf16 or f16");
+  if ((unsigned)w_dtype > TTCD_DTYPE_F32)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "unknown norm weight dtype");
+  if (!(eps >= 0.f) || !isfinite(eps))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+  const void* all[4] = {x, y, residual, residual_out};
+  for (int i = 0; i < 4; ++i)
+    if (all[i] && !aligned16(all[i]))
+      return fail(TTCD_ERR_UNSUPPORTED, "tensor base pointers must be 16-byte aligned");
+  if (w_dtype != TTCD_DTYPE_F32 && !aligned16(norm_w))
+    return fail(TTCD_ERR_UNSUPPORTED, "16-bit norm weights must be 16-byte aligned");
+  if (rows == 0) return ok();
+  return from_hip(ttcd::launch_dual_residual_rmsnorm(
+                      x, nullptr, residual, norm_w, elem(w_dtype), eps, y, residual_out, nullptr,
+                      rows, hidden, elem(dtype), static_cast<hipStream_t>(stream)),
+                  "rmsnorm launch");
+}
+
+ttcd_status ttcd_swiglu_fwd(const void* gate, const void* up, void* out, int64_t rows, int cols,
+                            int64_t gate_stride, int64_t up_stride, int64_t out_stride,
+                            ttcd_dtype dtype, void* stream) {
+  if (!gate || !up || !out) return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (rows < 0 || cols < 1) return fail(TTCD_ERR_INVALID_ARGUMENT, "need rows >= 0, cols >= 1");
+  if (gate_stride < cols || up_stride < cols || out_stride < cols)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "row strides must be >= cols");
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "dtype must be bf16 or f16");
+  if (cols % 8 != 0 || gate_stride % 8 != 0 || up_stride % 8 != 0 || out_stride % 8 != 0)
+    return fail(TTCD_ERR_UNSUPPORTED, "cols and row strides must be multiples of 8");
+  if (!aligned16(gate) || !aligned16(up) || !aligned16(out))
+    return fail(TTCD_ERR_UNSUPPORTED, "tensor base pointers must be 16-byte aligned");
+  if (rows == 0) return ok();
+  return from_hip(ttcd::launch_swiglu(gate, up, out, rows, cols, gate_stride, up_stride,
+                                      out_stride, elem(dtype), static_cast<hipStream_t>(stream)),
+                  "swiglu launch");
+}
+
+ttcd_status ttcd_ttt_features_fwd(const void* gu_t, const void* gu_s, int64_t gu_stride,
+                                  const void* conv_t, const void* conv_s, ttcd_dtype w_dtype,
+                                  int kernel_size, void* z, void* z_hat, void* diff, int B,
+                                  int nchunk, int chunk, int inter, ttcd_dtype dtype,
+                                  void* stream) {
+  if (!gu_t || !gu_s || !z || !z_hat || (nchunk > 1 && !diff))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (B < 1 || nchunk < 1 || chunk < 1 || inter < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need B, nchunk, chunk, inter >= 1");
+  if (gu_stride < 2 * (int64_t)inter)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "gate|up row stride must be >= 2 * inter");
+  if (kernel_size < 1 || ((conv_t || conv_s) && kernel_size > 8))
+    return fail(TTCD_ERR_UNSUPPORTED, "conv kernel size must be in 1..8");
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "dtype must be bf16 or f16");
+  if ((unsigned)w_dtype > TTCD_DTYPE_F32)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "unknown conv weight dtype");
+  if (inter % 8 != 0 || gu_stride % 8 != 0)
+    return fail(TTCD_ERR_UNSUPPORTED, "inter and the gate|up row stride must be multiples of 8");
+  const void* all[5] = {gu_t, gu_s, z, z_hat, diff};
+  for (int i = 0; i < 5; ++i)
+    if (all[i] && !aligned16(all[i]))
+      return fail(TTCD_ERR_UNSUPPORTED, "tensor base pointers must be 16-byte aligned");
+  ttcd::TttFeatureArgs a{gu_t, gu_s, gu_stride, conv_t, conv_s, (conv_t || conv_s) ? kernel_size : 1,
+                         z, z_hat, diff, B, nchunk, chunk, inter};
+  return from_hip(ttcd::launch_ttt_features(a, elem(dtype), elem(w_dtype),
+                                            static_cast<hipStream_t>(stream)),
+                  "ttt features launch");
+}
+
 ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int window_t,
                                         int gqa_group, int32_t* counts_near,
                                         int32_t* counts_far) {

@@ -16,6 +16,12 @@
 // the order of the sums of squares (lane-local in element order, then a
 // butterfly over the wavefront).
 //
+// The same kernel, with one branch, is the model's other RMSNorms: the
+// residual prenorm after a plain attention layer
+// (custom_models/ipttcd/modeling_ipttcdv9.py:863) and the plain RMSNorm of
+// attn_norm and of the final norm (:627, :1112; layernorm.py:189-251
+// without a residual).
+//
 // One wavefront per row: lane l owns the 16-byte chunks l, l + 64, ... of
 // the row, so every access is a coalesced 1 KiB transaction.
 #include <hip/hip_runtime.h>
@@ -49,10 +55,12 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// MAXC: 16-byte chunks per lane (H <= 512 * MAXC; the fp32 sums of both
-// branches stay in registers between the two passes, so H <= 2048).
-template <typename T, typename W, int MAXC>
-__global__ __launch_bounds__(256) void dual_residual_rmsnorm_kernel(
+// MAXC: 16-byte chunks per lane (H <= 512 * MAXC; the fp32 sums stay in
+// registers between the two passes, so H <= 2048). DUAL: a second (student)
+// branch on the same residual. RES: a residual is added (prenorm form, with
+// residual_out); without it the kernel is fla's plain RMSNorm of a.
+template <typename T, typename W, int MAXC, bool DUAL, bool RES>
+__global__ __launch_bounds__(256) void residual_rmsnorm_kernel(
     const T* __restrict__ a_t, const T* __restrict__ a_s, const T* __restrict__ res,
     const W* __restrict__ w, float eps, T* __restrict__ y_t, T* __restrict__ res_out,
     T* __restrict__ y_s, int64_t rows, int H) {
@@ -71,35 +79,35 @@ __global__ __launch_bounds__(256) void dual_residual_rmsnorm_kernel(
     vt.raw = vs.raw = vr.raw = u32x4{0u, 0u, 0u, 0u};
     if (ch < nch) {
       vt.raw = *reinterpret_cast<const u32x4*>(a_t + base + 8 * ch);
-      vs.raw = *reinterpret_cast<const u32x4*>(a_s + base + 8 * ch);
-      vr.raw = *reinterpret_cast<const u32x4*>(res + base + 8 * ch);
+      if (DUAL) vs.raw = *reinterpret_cast<const u32x4*>(a_s + base + 8 * ch);
+      if (RES) vr.raw = *reinterpret_cast<const u32x4*>(res + base + 8 * ch);
     }
     V8<T> ro;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float r = static_cast<float>(vr.e[e]);
-      xt[c][e] = static_cast<float>(vt.e[e]) + r;
-      xs[c][e] = static_cast<float>(vs.e[e]) + r;
-      ro.e[e] = round_to<T>(xt[c][e]);
+      const float r = RES ? static_cast<float>(vr.e[e]) : 0.f;
+      xt[c][e] = RES ? static_cast<float>(vt.e[e]) + r : static_cast<float>(vt.e[e]);
+      if (DUAL) xs[c][e] = static_cast<float>(vs.e[e]) + r;
+      if (RES) ro.e[e] = round_to<T>(xt[c][e]);
       sst = fmaf(xt[c][e], xt[c][e], sst);
-      sss = fmaf(xs[c][e], xs[c][e], sss);
+      if (DUAL) sss = fmaf(xs[c][e], xs[c][e], sss);
     }
-    if (ch < nch) *reinterpret_cast<u32x4*>(res_out + base + 8 * ch) = ro.raw;
+    if (RES && ch < nch) *reinterpret_cast<u32x4*>(res_out + base + 8 * ch) = ro.raw;
   }
   sst = wave_sum(sst);
-  sss = wave_sum(sss);
+  if (DUAL) sss = wave_sum(sss);
   const float rt = 1.0f / sqrtf(sst / (float)H + eps);
-  const float rs = 1.0f / sqrtf(sss / (float)H + eps);
+  const float rs = DUAL ? 1.0f / sqrtf(sss / (float)H + eps) : 0.f;
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
     const int ch = lane + 64 * c;
     if (ch >= nch) break;
-    V8<W> vw[1];
     float wf[8];
     if (sizeof(W) == 2) {
-      vw[0].raw = *reinterpret_cast<const u32x4*>(w + 8 * ch);
+      V8<W> vw;
+      vw.raw = *reinterpret_cast<const u32x4*>(w + 8 * ch);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) wf[e] = static_cast<float>(vw[0].e[e]);
+      for (int e = 0; e < 8; ++e) wf[e] = static_cast<float>(vw.e[e]);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) wf[e] = static_cast<float>(w[8 * ch + e]);
@@ -108,10 +116,10 @@ __global__ __launch_bounds__(256) void dual_residual_rmsnorm_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       ot.e[e] = round_to<T>((xt[c][e] * rt) * wf[e]);
-      os.e[e] = round_to<T>((xs[c][e] * rs) * wf[e]);
+      if (DUAL) os.e[e] = round_to<T>((xs[c][e] * rs) * wf[e]);
     }
     *reinterpret_cast<u32x4*>(y_t + base + 8 * ch) = ot.raw;
-    *reinterpret_cast<u32x4*>(y_s + base + 8 * ch) = os.raw;
+    if (DUAL) *reinterpret_cast<u32x4*>(y_s + base + 8 * ch) = os.raw;
   }
 }
 
@@ -119,11 +127,21 @@ template <typename T, typename W, int MAXC>
 hipError_t launch_c(const void* a_t, const void* a_s, const void* res, const void* w, float eps,
                     void* y_t, void* res_out, void* y_s, int64_t rows, int H, hipStream_t st) {
   const int64_t blocks = (rows + 3) / 4;
-  hipLaunchKernelGGL((dual_residual_rmsnorm_kernel<T, W, MAXC>), dim3((unsigned)blocks),
-                     dim3(256), 0, st, static_cast<const T*>(a_t), static_cast<const T*>(a_s),
-                     static_cast<const T*>(res), static_cast<const W*>(w), eps,
-                     static_cast<T*>(y_t), static_cast<T*>(res_out), static_cast<T*>(y_s), rows,
-                     H);
+  const bool dual = a_s != nullptr, has_res = res != nullptr;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st,
+                       static_cast<const T*>(a_t), static_cast<const T*>(a_s),
+                       static_cast<const T*>(res), static_cast<const W*>(w), eps,
+                       static_cast<T*>(y_t), static_cast<T*>(res_out), static_cast<T*>(y_s), rows,
+                       H);
+  };
+  if (dual) {
+    go(residual_rmsnorm_kernel<T, W, MAXC, true, true>);  // dual always has a residual
+  } else if (has_res) {
+    go(residual_rmsnorm_kernel<T, W, MAXC, false, true>);
+  } else {
+    go(residual_rmsnorm_kernel<T, W, MAXC, false, false>);
+  }
   return hipGetLastError();
 }
 

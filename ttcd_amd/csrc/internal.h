@@ -65,6 +65,26 @@ hipError_t launch_dual_residual_rmsnorm(const void* a_t, const void* a_s, const 
                                         void* res_out, void* y_s, int64_t rows, int H,
                                         Elem dtype, hipStream_t stream);
 
+// TTT MLP feature pass (ttt.hip). Rows are b-major, then chunk, then position.
+struct TttFeatureArgs {
+  const void* gu_t;  // teacher (rows, 2*I) gate | up, row stride gu_st
+  const void* gu_s;  // student, same layout
+  int64_t gu_st;
+  const void* w_t;   // teacher conv weight (I, K) or null
+  const void* w_s;   // student conv weight (I, K) or null
+  int K;
+  void* z;           // (rows, I) teacher features
+  void* z_hat;       // (rows, I) student features after the student conv
+  void* diff;        // (B * (nchunk - 1) * C, I)
+  int B, nchunk, C, I;
+};
+
+hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t rows, int cols,
+                         int64_t gate_stride, int64_t up_stride, int64_t out_stride, Elem dtype,
+                         hipStream_t stream);
+hipError_t launch_ttt_features(const TttFeatureArgs& a, Elem dtype, Elem w_dtype,
+                               hipStream_t stream);
+
 hipError_t launch_dwconv(const void* x, const void* w, void* y, int64_t N, int C,
                          int D, int K, Elem xt, Elem wt, hipStream_t stream);
 

@@ -16,6 +16,8 @@ twice and also store the student's discarded residual sum), with one GEMM
 
     dual_residual_rmsnorm(attn_t, attn_s, residual, weight, eps)
         -> (hidden_states, residual_out, student_output)
+    rmsnorm(x, weight, eps, residual=None)
+        -> y, or (y, x + residual) with a residual (the model's other norms)
     fused_attn_epilogue(o_proj, mlp_norm, o_t, o_s, residual)
         drop-in for the call site above
 """
@@ -57,7 +59,11 @@ def dual_residual_rmsnorm(attn_t: torch.Tensor, attn_s: torch.Tensor, residual: 
                            "are not supported; call it under torch.no_grad()")
     a_t, a_s, res = attn_t.contiguous(), attn_s.contiguous(), residual.contiguous()
     w = weight.contiguous()
-    y_t, res_out, y_s = torch.empty_like(res), torch.empty_like(res), torch.empty_like(res)
+    # hidden_states and student_output are the two halves of one allocation, so
+    # the TTT MLP can run its gate/up GEMM over both without a copy
+    ys = torch.empty((2,) + tuple(res.shape), dtype=res.dtype, device=res.device)
+    y_t, y_s = ys[0], ys[1]
+    res_out = torch.empty_like(res)
     rows = res.numel() // H if H > 0 else 0
     if rows == 0:  # nothing to launch (an empty tensor's data pointer may be null)
         return y_t, res_out, y_s
@@ -66,6 +72,44 @@ def dual_residual_rmsnorm(attn_t: torch.Tensor, attn_s: torch.Tensor, residual: 
         y_t.data_ptr(), res_out.data_ptr(), y_s.data_ptr(), rows, H, _DT[res.dtype],
         torch.cuda.current_stream(res.device).cuda_stream))
     return y_t, res_out, y_s
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """fla's RMSNorm forward (fla/modules/layernorm.py:189-251, 715-764) on the
+    GPU: ``RMSNorm(x) * weight`` rounded to x's dtype, or, with a residual, the
+    prenorm form returning ``(RMSNorm(x + residual) * weight, x + residual)``
+    with the variance of the unrounded fp32 sum. ``out`` (optional) receives y."""
+    for name, t in (("x", x), ("weight", weight)) + ((("residual", residual),) if residual is not None else ()):
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise ValueError(f"rmsnorm: {name} must be a tensor on a GPU (HIP) device")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("rmsnorm: x must be bf16 or f16")
+    H = x.shape[-1]
+    if weight.shape != (H,) or weight.dtype not in _DT:
+        raise ValueError(f"rmsnorm: weight must be ({H},) of bf16, f16 or f32")
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype):
+        raise ValueError("rmsnorm: residual must match x in shape and dtype")
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, residual, weight)):
+        raise RuntimeError("rmsnorm is forward-only: call it under torch.no_grad()")
+    x = x.contiguous()
+    res = residual.contiguous() if residual is not None else None
+    w = weight.contiguous()
+    if out is None:
+        y = torch.empty_like(x)
+    else:
+        if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+            raise ValueError("rmsnorm: out must be contiguous and match x")
+        y = out
+    res_out = torch.empty_like(x) if res is not None else None
+    rows = x.numel() // H if H > 0 else 0
+    if rows > 0:
+        _lib.check(_lib.lib().ttcd_rmsnorm_fwd(
+            x.data_ptr(), res.data_ptr() if res is not None else None, w.data_ptr(),
+            _DT[w.dtype], float(eps), y.data_ptr(),
+            res_out.data_ptr() if res_out is not None else None, rows, H, _DT[x.dtype],
+            torch.cuda.current_stream(x.device).cuda_stream))
+    return y if res is None else (y, res_out)
 
 
 def _stacked(o_t: torch.Tensor, o_s: torch.Tensor) -> torch.Tensor:

@@ -1,0 +1,321 @@
+"""Prefill of an ipttcdv9 (IP-TTCD) model on gfx950, end to end.
+
+A forward-only restatement of IPTTCDForCausalLM's prefill
+(custom_models/ipttcd/modeling_ipttcdv9.py:577-880, 999-1128, 1194-1241),
+with the TTT MLP of modeling_ipttcdv9_lowcopy_scanfuse.py:36-204 (what
+profiling/bench_prefill.py runs by default) and the two patches that
+`bench_prefill.py --patch fused_conv` installs (profiling/patches.py:
+215-312 fused dual-window attention on the TTT layers, 411-432 chunk-local
+conv). It runs no reference code: parameters are held under the reference's
+state-dict names, and every step calls this package's HIP kernels or a
+hipBLASLt GEMM through torch.
+
+Per layer (attn_norm = fla RMSNorm; qk_norm + rotary; window W_T):
+  plain layer: h -> RMSNorm -> one q|k|v GEMM -> q/k RMSNorm + rotary (one
+      kernel) -> band attention (window W_T) -> o_proj -> residual RMSNorm
+      -> gate|up GEMM -> SwiGLU -> down GEMM -> residual add
+  TTT layer:   ... -> fused dual-window attention (W_T, W_S = visible chunks
+      x ttt_chunk) -> one o_proj GEMM over both outputs -> dual residual
+      RMSNorm -> TTT MLP (ttcd_amd.ttt.ttt_mlp) -> residual add
+then the final RMSNorm and the LM head on the last `logits_to_keep` tokens.
+
+`fused=False` is the unpatched shape of the reference's prefill fast path
+(modeling_ipttcdv9.py:682-781): two windowed attention calls (this package's
+band kernel), two o_proj GEMMs and two norms, and the TTT feature pass as
+separate SwiGLU / conv / subtraction launches. Both modes use the same
+kernels for everything else, so their difference is what the fused kernels
+buy end to end.
+
+Not covered (raise NotImplementedError): use_output_gate, qkv_bias,
+non-causal TTT conv, ttt_weight_renorm, Muon, normalised TTT features or
+proj-diff, ttt_output_use_teacher_conv, a KV cache (prefill only; the
+reference's cache writes are copies of k and v).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from . import attn as _attn
+from . import epilogue as _epi
+from . import prologue as _pro
+from . import ttt as _ttt
+
+# configs/ipttcd/ipttcdv9_qwen3_0.6B_ct_64k_v2_swa8k.json (the config-5 model)
+QWEN3_06B_SWA8K = {
+    "hidden_size": 1024, "num_hidden_layers": 28, "num_heads": 16, "num_kv_heads": 8,
+    "head_dim": 128, "intermediate_size": 3072, "vocab_size": 151936,
+    "max_position_embeddings": 65536, "rope_theta": 1000000.0, "window_size": 8192,
+    "norm_eps": 1e-06, "initializer_range": 0.02, "tie_word_embeddings": True,
+    "qkv_bias": False, "qk_norm": True, "fuse_norm": True, "fuse_swiglu": True,
+    "ttt_mode": True, "ttt_layers": [0, 7, 14, 21], "ttt_chunk": 4096, "ttt_lr": 0.3,
+    "ttt_proj": True, "ttt_proj_init": "diagonal_gaussian", "ttt_norm_proj_diff": False,
+    "ttt_normalize_student_features": False, "ttt_conv": True, "ttt_teacher_conv": True,
+    "ttt_student_conv": True, "ttt_teacher_conv_init": "identity",
+    "ttt_student_conv_init": "zero", "ttt_output_use_teacher_conv": False,
+    "ttt_conv_kernel_size": 5, "ttt_conv_causal": True, "dynamic_lr": True,
+    "ttt_visible_chunks": 1, "ttt_update_every": 16, "ttt_weight_renorm": False,
+    "use_muon": False,
+}
+
+# the reference config classes' defaults for keys a config file may omit
+# (configuration_ipttcd.py:16-65, configuration_ipttcdv8.py:12-19,
+# configuration_ipttcdv9.py:12-17)
+_DEFAULTS = {
+    "num_kv_heads": None, "head_dim": None, "qkv_bias": False, "qk_norm": False,
+    "window_size": None, "rope_theta": 10000.0, "max_position_embeddings": 2048,
+    "hidden_ratio": 4, "intermediate_size": None, "norm_eps": 1e-6,
+    "initializer_range": 0.02, "tie_word_embeddings": False, "use_output_gate": False,
+    "ttt_mode": False, "ttt_layers": None, "ttt_chunk": 8192, "ttt_lr": 0.3, "ttt_proj": True,
+    "ttt_proj_init": "diagonal", "ttt_conv": False, "ttt_teacher_conv": True,
+    "ttt_student_conv": True, "ttt_conv_kernel_size": 5, "ttt_conv_causal": True,
+    "ttt_teacher_conv_init": "zero", "ttt_student_conv_init": "zero",
+    "ttt_output_use_teacher_conv": True, "ttt_output_source": "teacher", "dynamic_lr": True,
+    "ttt_visible_chunks": 1, "use_muon": False, "ttt_weight_renorm": False,
+    "ttt_norm_proj_diff": False, "ttt_normalize_student_features": True,
+    "ttt_update_every": 4, "ttt_fuse_proj_into_update": True,
+}
+
+
+def resolve_config(cfg: dict) -> dict:
+    """The reference config with its defaults filled in and the derived sizes
+    (num_kv_heads, head_dim, intermediate_size) computed as the reference's
+    modules do (fla/layers/attn.py; modeling_ipttcdv9.py:98-102)."""
+    c = dict(_DEFAULTS)
+    c.update(cfg)
+    c["num_kv_heads"] = c["num_kv_heads"] or c["num_heads"]
+    c["head_dim"] = c["head_dim"] or c["hidden_size"] // c["num_heads"]
+    if c["intermediate_size"] is None:
+        inter = int(c["hidden_size"] * c["hidden_ratio"] * 2 / 3)
+        c["intermediate_size"] = 256 * ((inter + 256 - 1) // 256)
+    c["ttt_layers"] = list(c["ttt_layers"] or []) if c["ttt_mode"] else []
+    # the MLP reads ttt_teacher_conv / ttt_student_conv directly; ttt_conv is
+    # only their OR (configuration_ipttcdv8.py:32-34, modeling_ipttcdv9.py:130-150)
+    c["ttt_teacher_conv"] = bool(c["ttt_teacher_conv"])
+    c["ttt_student_conv"] = bool(c["ttt_student_conv"])
+    unsupported = [k for k, bad in (
+        ("use_output_gate", c["use_output_gate"]), ("qkv_bias", c["qkv_bias"]),
+        ("ttt_conv_causal=False", c["ttt_layers"] and not c["ttt_conv_causal"]),
+        ("ttt_weight_renorm", c["ttt_weight_renorm"]), ("use_muon", c["use_muon"]),
+        ("ttt_normalize_student_features", c["ttt_layers"] and c["ttt_normalize_student_features"]),
+        ("ttt_norm_proj_diff", c["ttt_norm_proj_diff"]),
+        ("ttt_output_use_teacher_conv", c["ttt_layers"] and c["ttt_output_use_teacher_conv"]),
+        ("ttt_output_source", c["ttt_output_source"] != "teacher"),
+        ("ttt_fuse_proj_into_update=False", not c["ttt_fuse_proj_into_update"])) if bad]
+    if unsupported:
+        raise NotImplementedError(f"ipttcdv9 prefill: unsupported options {unsupported}")
+    return c
+
+
+def init_weights(cfg: dict, device, dtype=torch.bfloat16, seed: int = 0) -> dict:
+    """Random parameters with the reference's initialisation
+    (modeling_ipttcdv9.py:885-996 over fla's TransformerPreTrainedModel
+    init): Linear and Embedding N(0, initializer_range); norms ones; ttt_proj
+    per ttt_proj_init; TTT convs per ttt_{teacher,student}_conv_init; b_proj
+    N(0, initializer_range). Drawn in fp32 on `device` from `seed`, then cast
+    to `dtype` (as build_model casts the fp32 model, bench_prefill.py:76-77)."""
+    c = resolve_config(cfg)
+    g = torch.Generator(device=device).manual_seed(seed)
+    std = c["initializer_range"]
+    H, I, D = c["hidden_size"], c["intermediate_size"], c["head_dim"]
+    Hq, Hkv, K = c["num_heads"], c["num_kv_heads"], c["ttt_conv_kernel_size"]
+
+    def normal(*shape):
+        return (torch.randn(*shape, generator=g, device=device) * std).to(dtype)
+
+    def ones(n):
+        return torch.ones(n, device=device, dtype=dtype)
+
+    w = {"model.embeddings.weight": normal(c["vocab_size"], H)}
+    for i in range(c["num_hidden_layers"]):
+        p = f"model.layers.{i}."
+        w[p + "attn_norm.weight"] = ones(H)
+        w[p + "attn.q_proj.weight"] = normal(Hq * D, H)
+        w[p + "attn.k_proj.weight"] = normal(Hkv * D, H)
+        w[p + "attn.v_proj.weight"] = normal(Hkv * D, H)
+        w[p + "attn.o_proj.weight"] = normal(H, Hq * D)
+        if c["qk_norm"]:
+            w[p + "attn.q_norm.weight"] = ones(D)
+            w[p + "attn.k_norm.weight"] = ones(D)
+        w[p + "mlp_norm.weight"] = ones(H)
+        w[p + "mlp.gate_proj.weight"] = normal(I, H)
+        w[p + "mlp.up_proj.weight"] = normal(I, H)
+        w[p + "mlp.down_proj.weight"] = normal(H, I)
+        if i in c["ttt_layers"]:
+            if c["ttt_proj"]:
+                init = c["ttt_proj_init"]
+                if init == "diagonal":
+                    pw = torch.eye(H, device=device) * std
+                elif init == "diagonal_gaussian":
+                    pw = torch.diag(torch.randn(H, generator=g, device=device) * std)
+                elif init == "zero":
+                    pw = torch.zeros(H, H, device=device)
+                else:
+                    pw = torch.randn(H, H, generator=g, device=device) * std
+                w[p + "mlp.ttt_proj.weight"] = pw.to(dtype)
+            for role in ("teacher", "student"):
+                if not c[f"ttt_{role}_conv"]:
+                    continue
+                init = c[f"ttt_{role}_conv_init"]
+                cw = torch.zeros(I, 1, K, device=device)
+                if init == "identity":
+                    cw[:, 0, K - 1] = 1.0  # causal conv: the last tap is the current position
+                elif init == "random":
+                    cw = torch.randn(I, 1, K, generator=g, device=device) * std
+                w[p + f"mlp.ttt_{role}_conv.weight"] = cw.to(dtype)
+            if c["dynamic_lr"]:
+                w[p + "mlp.b_proj"] = normal(H)
+    w["model.norm.weight"] = ones(H)
+    w["lm_head.weight"] = (w["model.embeddings.weight"] if c["tie_word_embeddings"]
+                           else normal(c["vocab_size"], H))
+    return w
+
+
+class IPTTCDv9Prefill:
+    """Prefill-only ipttcdv9 on one GPU. `weights` uses the reference's
+    state-dict names (e.g. from init_weights, or a safetensors checkpoint of the
+    reference model cast to bf16)."""
+
+    def __init__(self, cfg: dict, weights: dict):
+        self.cfg = c = resolve_config(cfg)
+        self.w = weights
+        self.dev = weights["model.embeddings.weight"].device
+        self.dtype = weights["model.embeddings.weight"].dtype
+        H, D = c["hidden_size"], c["head_dim"]
+        self.Hq, self.Hkv, self.D = c["num_heads"], c["num_kv_heads"], D
+        # stacked projection weights: one GEMM for q|k|v, one for gate|up
+        self.qkv_w, self.gu_w, self.ttt = [], [], {}
+        for i in range(c["num_hidden_layers"]):
+            p = f"model.layers.{i}."
+            self.qkv_w.append(torch.cat([weights[p + "attn.q_proj.weight"],
+                                         weights[p + "attn.k_proj.weight"],
+                                         weights[p + "attn.v_proj.weight"]], 0).contiguous())
+            self.gu_w.append(torch.cat([weights[p + "mlp.gate_proj.weight"],
+                                        weights[p + "mlp.up_proj.weight"]], 0).contiguous())
+            if i in c["ttt_layers"]:
+                self.ttt[i] = _ttt.TttMlpWeights(
+                    self.gu_w[i], weights[p + "mlp.down_proj.weight"],
+                    weights.get(p + "mlp.ttt_proj.weight"),
+                    weights.get(p + "mlp.ttt_teacher_conv.weight"),
+                    weights.get(p + "mlp.ttt_student_conv.weight"),
+                    weights.get(p + "mlp.b_proj"))
+        # rotary tables of the reference's cache length (max_seqlen is at least
+        # max_position_embeddings, fla/layers/attn.py:200-213), from fp32 inv_freq
+        self._inv_freq = _pro.rope_inv_freq(D, c["rope_theta"], self.dev)
+        self._tables = None
+        self.window_t = c["window_size"] if c["window_size"] is not None else -1
+        self.window_s = c["ttt_visible_chunks"] * c["ttt_chunk"]
+
+    def tables(self, T: int):
+        rows = max(T, self.cfg["max_position_embeddings"] or 0)
+        if self._tables is None or self._tables[0].shape[0] < rows:
+            self._tables = _pro.rope_tables(self._inv_freq, rows, self.dtype)
+        return self._tables
+
+    # ------------------------------------------------------------------ layers
+
+    def _qkv(self, i: int, x: torch.Tensor):
+        c, w = self.cfg, self.w
+        B, T, _ = x.shape
+        Hq, Hkv, D = self.Hq, self.Hkv, self.D
+        qkv = F.linear(x, self.qkv_w[i])
+        q = qkv[..., :Hq * D].view(B, T, Hq, D)
+        k = qkv[..., Hq * D:(Hq + Hkv) * D].view(B, T, Hkv, D)
+        v = qkv[..., (Hq + Hkv) * D:].view(B, T, Hkv, D)
+        p = f"model.layers.{i}.attn."
+        cos, sin = self.tables(T)
+        qw = w.get(p + "q_norm.weight") if c["qk_norm"] else None
+        kw = w.get(p + "k_norm.weight") if c["qk_norm"] else None
+        # fla's RMSNorm default eps for q_norm / k_norm (fla/layers/attn.py:61-63)
+        q, k = _pro.qk_norm_rope(q, k, qw, kw, 1e-5, cos, sin, 0)
+        return q, k, v
+
+    def layer(self, i: int, h: torch.Tensor, fused: bool = True) -> torch.Tensor:
+        c, w = self.cfg, self.w
+        p = f"model.layers.{i}."
+        eps = c["norm_eps"]
+        B, T, H = h.shape
+        residual = h
+        x = _epi.rmsnorm(h, w[p + "attn_norm.weight"], eps)
+        q, k, v = self._qkv(i, x)
+        o_w = w[p + "attn.o_proj.weight"]
+        if i in self.ttt and T >= c["ttt_chunk"]:
+            norm = _NormView(w[p + "mlp_norm.weight"], eps)
+            proj = _LinearView(o_w)
+            if fused:
+                o_t, o_s = _attn.fused_dual_window_attn(q, k, v, self.window_t, self.window_s)
+                x, residual, s = _epi.fused_attn_epilogue(proj, norm, o_t, o_s, residual)
+            else:
+                o_t = _attn.window_attn(q, k, v, self.window_t)
+                o_s = _attn.window_attn(q, k, v, self.window_s)
+                a_t = F.linear(o_t.reshape(B, T, -1), o_w)
+                a_s = F.linear(o_s.reshape(B, T, -1), o_w)
+                s, _ = _epi.rmsnorm(a_s, w[p + "mlp_norm.weight"], eps, residual=residual)
+                x, residual = _epi.rmsnorm(a_t, w[p + "mlp_norm.weight"], eps, residual=residual)
+            y = _ttt.ttt_mlp(x, s, self.ttt[i], chunk=c["ttt_chunk"], lr=c["ttt_lr"],
+                             update_every=c["ttt_update_every"], fused=fused)
+        else:
+            o = _attn.window_attn(q, k, v, self.window_t)
+            a = F.linear(o.reshape(B, T, -1), o_w)
+            x, residual = _epi.rmsnorm(a, w[p + "mlp_norm.weight"], eps, residual=residual)
+            y = _ttt.swiglu_mlp(x, self.gu_w[i], w[p + "mlp.down_proj.weight"])
+        return residual + y
+
+    @torch.inference_mode()
+    def forward(self, input_ids: torch.Tensor, logits_to_keep: int = 1,
+                fused: bool = True) -> torch.Tensor:
+        """Logits (B, logits_to_keep, vocab) of the prefill of `input_ids`
+        (B, T), as IPTTCDForCausalLM(input_ids, logits_to_keep=...) returns them
+        with fuse_linear_cross_entropy off (bench_prefill.py:73-74)."""
+        if input_ids.dim() != 2 or input_ids.device != self.dev:
+            raise ValueError("input_ids must be (B, T) on the model's device")
+        h = F.embedding(input_ids, self.w["model.embeddings.weight"])
+        for i in range(self.cfg["num_hidden_layers"]):
+            h = self.layer(i, h, fused)
+        keep = h[:, -logits_to_keep:] if logits_to_keep > 0 else h
+        x = _epi.rmsnorm(keep.contiguous(), self.w["model.norm.weight"], self.cfg["norm_eps"])
+        return F.linear(x, self.w["lm_head.weight"])
+
+
+class _NormView:
+    """The attributes of an fla RMSNorm module that fused_attn_epilogue reads."""
+
+    def __init__(self, weight, eps):
+        self.weight, self.bias, self.eps = weight, None, eps
+
+
+class _LinearView:
+    def __init__(self, weight):
+        self.weight, self.bias = weight, None
+
+
+def prefill_flops(cfg: dict, B: int, T: int) -> dict:
+    """Algorithmic FLOPs of one prefill by part (GEMMs 2*m*n*k; attention
+    4*Hq*D per in-band pair, the teacher band once on TTT layers)."""
+    from math import ceil
+    c = resolve_config(cfg)
+    H, I, D = c["hidden_size"], c["intermediate_size"], c["head_dim"]
+    Hq, Hkv, L = c["num_heads"], c["num_kv_heads"], c["num_hidden_layers"]
+    n_ttt = sum(1 for i in c["ttt_layers"] if i < L)
+    W = c["window_size"]
+
+    def pairs(W):
+        if W is None or W >= T:
+            return T * (T + 1) // 2
+        return W * (W + 1) // 2 + (T - W) * W
+
+    tok = B * T
+    proj = 2 * tok * H * (Hq + 2 * Hkv) * D + 2 * tok * Hq * D * H
+    mlp = 2 * tok * H * 2 * I + 2 * tok * I * H
+    attn = 4 * B * Hq * D * pairs(W)
+    C = c["ttt_chunk"]
+    nch = ceil(T / C)
+    ttt_extra = (2 * tok * Hq * D * H            # student o_proj
+                 + 2 * tok * H * 2 * I           # student gate|up
+                 + 2 * B * (nch - 1) * C * I * H  # diff @ W_update
+                 + 2 * B * (nch - 1) * H * C * I  # dW
+                 + 2 * I * H * H)                # W_update = W_down^T @ P
+    return {"gemm": L * (proj + mlp) + n_ttt * ttt_extra, "attention": L * attn,
+            "lm_head": 2 * B * H * c["vocab_size"]}
