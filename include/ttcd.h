@@ -48,7 +48,8 @@ const char* ttcd_last_error(void);
 int ttcd_abi_version(void);
 
 /*
- * One-pass dual-window causal GQA attention (forward, prefill, Tq == Tk).
+ * One-pass dual-window causal GQA attention (forward, prefill, Tq == Tk;
+ * ttcd_dual_window_attn_kv_fwd below takes Tq <= Tk).
  * Replaces fused_dual_window_attn / _fused_dual_swa_fwd
  * (profiling/fused_dual_attn.py:244-272, kernel :44-241).
  *
@@ -79,6 +80,29 @@ ttcd_status ttcd_dual_window_attn_fwd(
 ttcd_status ttcd_band_attn_fwd(
     const void* q, const void* k, const void* v, void* o, float* lse, int B,
     int T, int Hq, int Hkv, int D, const int64_t q_stride[4],
+    const int64_t k_stride[4], const int64_t v_stride[4],
+    const int64_t o_stride[4], int band_lo, int band_hi, float sm_scale,
+    ttcd_dtype dtype, void* stream);
+
+/*
+ * Cached prefill (Tq <= Tk): the same two calls for Tq new query rows against
+ * Tk keys, the queries at absolute positions Tk - Tq .. Tk - 1 (the bottom-
+ * right aligned causal mask of flash_attn_func with seqlen_q < seqlen_k, as
+ * test/test_fused_dual_attn.py:275-293 specifies for fused_dual_window_attn,
+ * where the reference kernel is a strict xfail). q, o_t, o_s, o: (B, Tq, Hq,
+ * D); k, v: (B, Tk, Hkv, D); lse*: (B, Hq, Tq). Windows, bands and every
+ * other argument as above; with Tq == Tk these are the calls above.
+ */
+ttcd_status ttcd_dual_window_attn_kv_fwd(
+    const void* q, const void* k, const void* v, void* o_t, void* o_s,
+    float* lse_t, float* lse_s, int B, int Tq, int Tk, int Hq, int Hkv, int D,
+    const int64_t q_stride[4], const int64_t k_stride[4],
+    const int64_t v_stride[4], const int64_t o_stride[4], int window_t,
+    int window_s, float sm_scale, ttcd_dtype dtype, void* stream);
+
+ttcd_status ttcd_band_attn_kv_fwd(
+    const void* q, const void* k, const void* v, void* o, float* lse, int B,
+    int Tq, int Tk, int Hq, int Hkv, int D, const int64_t q_stride[4],
     const int64_t k_stride[4], const int64_t v_stride[4],
     const int64_t o_stride[4], int band_lo, int band_hi, float sm_scale,
     ttcd_dtype dtype, void* stream);

@@ -170,6 +170,23 @@ def test_prefill_matches_oracle(T):
     _logits_close(got, got2, max_frac=2e-2, mean_frac=1e-2)
 
 
+# SmolLM2-360M's attention shape (configs/ipttcd/ipttcdv9_smollm2_360M_ct_64k_v2_swa8k.json):
+# 15 query / 5 KV heads of 64, no qk_norm, rope_theta 1e5, norm_eps 1e-5
+SMOL = dict(TINY, hidden_size=960, num_heads=15, num_kv_heads=5, head_dim=64, qk_norm=False,
+            rope_theta=100000.0, norm_eps=1e-05, intermediate_size=640, ttt_layers=[1])
+
+
+def test_prefill_smollm2_shape_matches_oracle():
+    c = M.resolve_config(SMOL)
+    w = M.init_weights(SMOL, DEV, seed=2)
+    model = M.IPTTCDv9Prefill(SMOL, w)
+    ids = torch.randint(0, c["vocab_size"], (1, 768), generator=torch.Generator().manual_seed(7))
+    got = model.forward(ids.to(DEV), logits_to_keep=8)
+    torch.cuda.synchronize()
+    want = R.prefill_ref(c, {k: v.cpu() for k, v in w.items()}, ids, 8, torch.bfloat16)
+    _logits_close(got, want)
+
+
 def test_prefill_batch_rows_are_independent():
     c = M.resolve_config(TINY)
     w = M.init_weights(TINY, DEV, seed=1)

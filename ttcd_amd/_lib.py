@@ -31,6 +31,8 @@ EXPORTS = (
     "ttcd_abi_version",
     "ttcd_dual_window_attn_fwd",
     "ttcd_band_attn_fwd",
+    "ttcd_dual_window_attn_kv_fwd",
+    "ttcd_band_attn_kv_fwd",
     "ttcd_lse_merge_fwd",
     "ttcd_causal_dwconv_chunked_fwd",
     "ttcd_qk_norm_rope_fwd",
@@ -60,6 +62,16 @@ _SIGS = {
     "ttcd_band_attn_fwd": (_i32, [
         _vp, _vp, _vp, _vp, _fp,
         _i32, _i32, _i32, _i32, _i32,
+        _i64x4, _i64x4, _i64x4, _i64x4,
+        _i32, _i32, ctypes.c_float, _i32, _vp]),
+    "ttcd_dual_window_attn_kv_fwd": (_i32, [
+        _vp, _vp, _vp, _vp, _vp, _fp, _fp,
+        _i32, _i32, _i32, _i32, _i32, _i32,
+        _i64x4, _i64x4, _i64x4, _i64x4,
+        _i32, _i32, ctypes.c_float, _i32, _vp]),
+    "ttcd_band_attn_kv_fwd": (_i32, [
+        _vp, _vp, _vp, _vp, _fp,
+        _i32, _i32, _i32, _i32, _i32, _i32,
         _i64x4, _i64x4, _i64x4, _i64x4,
         _i32, _i32, ctypes.c_float, _i32, _vp]),
     "ttcd_lse_merge_fwd": (_i32, [

@@ -42,9 +42,10 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, fn: str):
     if not (q.device == k.device == v.device):
         raise ValueError(f"{fn}: q, k, v must be on one device")
     B, T, H, D = q.shape
-    if k.shape != v.shape or k.shape[0] != B or k.shape[1] != T or k.shape[3] != D:
-        raise ValueError(f"{fn}: k/v must be (B, T, Hkv, D) matching q {tuple(q.shape)}, "
-                         f"got {tuple(k.shape)} / {tuple(v.shape)}")
+    # Tk > Tq: a cached prefill, queries at the last Tq key positions
+    if k.shape != v.shape or k.shape[0] != B or k.shape[1] < T or k.shape[3] != D:
+        raise ValueError(f"{fn}: k/v must be (B, Tk, Hkv, D) with Tk >= Tq, matching q "
+                         f"{tuple(q.shape)}, got {tuple(k.shape)} / {tuple(v.shape)}")
     HK = k.shape[2]
     if H % HK != 0:
         raise ValueError(f"{fn}: Hq ({H}) must be a multiple of Hkv ({HK})")
@@ -81,10 +82,15 @@ def fused_dual_window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     any value >= 1 and teacher == student windows of any alignment are exact.
     With ``return_lse=True`` also returns (lse_teacher, lse_student), fp32
     natural-log (B, H, T).
+
+    k / v may be longer than q (Tk > Tq, a prefill onto a populated cache):
+    the queries are then the last Tq positions, flash-attention's
+    bottom-right aligned causal mask, which test/test_fused_dual_attn.py:
+    275-293 asks of this call (a strict xfail for the reference kernel).
     """
-    T = q.shape[1]
+    Tk = k.shape[1] if isinstance(k, torch.Tensor) and k.dim() == 4 else q.shape[1]
     if window_teacher is None or window_teacher < 0:
-        window_teacher = T
+        window_teacher = Tk
     assert window_student <= window_teacher
     assert window_student >= 1, "window_student must be >= 1"
     if int(block_n) <= 0:
@@ -100,9 +106,9 @@ def fused_dual_window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         lse_t = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
         lse_s = torch.empty(B, H, T, device=q.device, dtype=torch.float32)
     L = _lib.lib()
-    _lib.check(L.ttcd_dual_window_attn_fwd(
+    _lib.check(L.ttcd_dual_window_attn_kv_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), ot.data_ptr(), os_.data_ptr(),
-        _lse_ptr(lse_t), _lse_ptr(lse_s), B, T, H, HK, D,
+        _lse_ptr(lse_t), _lse_ptr(lse_s), B, T, k.shape[1], H, HK, D,
         _lib.strides4(q.stride()), _lib.strides4(k.stride()), _lib.strides4(v.stride()),
         _lib.strides4(ot.stride()), int(min(window_teacher, 2**31 - 1)),
         int(min(window_student, 2**31 - 1)), D ** -0.5, _DT[q.dtype], _stream(q.device)))
@@ -120,17 +126,18 @@ def band_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, band_lo: int, b
     whose band is empty get o = 0 and lse = -inf.
     """
     B, T, H, HK, D = _check_qkv(q, k, v, "band_attn")
+    Tk = k.shape[1]
     if band_hi is None or band_hi < 0:
-        band_hi = max(T, band_lo + 1)
+        band_hi = max(Tk, band_lo + 1)
     if not (0 <= band_lo < band_hi):
         raise ValueError(f"band_attn: need 0 <= band_lo < band_hi, got ({band_lo}, {band_hi})")
     q, k, v = _ready(q), _ready(k), _ready(v)
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, T, device=q.device, dtype=torch.float32) if return_lse else None
     L = _lib.lib()
-    _lib.check(L.ttcd_band_attn_fwd(
+    _lib.check(L.ttcd_band_attn_kv_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), _lse_ptr(lse),
-        B, T, H, HK, D,
+        B, T, Tk, H, HK, D,
         _lib.strides4(q.stride()), _lib.strides4(k.stride()), _lib.strides4(v.stride()),
         _lib.strides4(o.stride()), int(min(band_lo, 2**31 - 1)), int(min(band_hi, 2**31 - 1)),
         D ** -0.5, _DT[q.dtype], _stream(q.device)))
@@ -140,8 +147,10 @@ def band_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, band_lo: int, b
 def window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int | None,
                 *, return_lse: bool = False):
     """flash_attn_func(q, k, v, causal=True, window_size=(window-1, 0)) on gfx950;
-    window None or < 0 = full causal. The "two separate calls" comparator."""
-    T = q.shape[1]
+    window None or < 0 = full causal. The "two separate calls" comparator.
+    With k / v longer than q (a cached prefill), the queries are the last Tq
+    positions (flash-attention's bottom-right alignment)."""
+    T = k.shape[1] if isinstance(k, torch.Tensor) and k.dim() == 4 else q.shape[1]
     w = T if (window is None or window < 0) else window
     if w < 1:
         raise ValueError("window must be >= 1")
@@ -176,15 +185,17 @@ def lse_dual_window_attn(q, k, v, window_teacher: int, window_student: int):
     """Student = window WS (with LSE); far band [WS, WT) (with LSE); teacher =
     exact LSE merge. profiling/lse_dual_attn.py:16-39 (flash-attn there, the
     gfx950 band kernel here). Requires WS < WT (AssertionError otherwise)."""
-    B, T, H, D = q.shape
-    WT = T if (window_teacher is None or window_teacher < 0) else window_teacher
+    B, Tq, H, D = q.shape
+    Tk = k.shape[1]
+    WT = Tk if (window_teacher is None or window_teacher < 0) else window_teacher
     WS = window_student
     assert WS < WT
     o_s, lse_s = window_attn(q, k, v, WS, return_lse=True)
-    if T <= WS:
+    if Tk <= WS:
         return o_s, o_s
     o_f, lse_f = band_attn(q, k, v, WS, WT, return_lse=True)
-    o_t = lse_merge(o_s, lse_s, o_f, lse_f, row_start=WS)
+    # rows at absolute positions below WS have an empty far band
+    o_t = lse_merge(o_s, lse_s, o_f, lse_f, row_start=max(0, WS - (Tk - Tq)))
     return o_t, o_s
 
 

@@ -92,6 +92,8 @@ ttcd::AttnArgs fill_args(const void* q, const void* k, const void* v, int B, int
   a.Hkv = Hkv;
   a.G = Hq / Hkv;
   const int span = ttcd::wg_span_tokens(a.G);
+  a.q_off = 0;
+  a.qb0 = 0;
   a.nqb = (T + span - 1) / span;  // query blocks per (b, slice)
   a.c = sm_scale * 1.4426950408889634f;
   return a;
@@ -120,33 +122,85 @@ const char* ttcd_last_error(void) { return g_err; }
 
 int ttcd_abi_version(void) { return TTCD_ABI_VERSION; }
 
-ttcd_status ttcd_dual_window_attn_fwd(const void* q, const void* k, const void* v, void* o_t,
-                                      void* o_s, float* lse_t, float* lse_s, int B, int T,
-                                      int Hq, int Hkv, int D, const int64_t q_stride[4],
-                                      const int64_t k_stride[4], const int64_t v_stride[4],
-                                      const int64_t o_stride[4], int window_t, int window_s,
-                                      float sm_scale, ttcd_dtype dtype, void* stream) {
+// Tq query rows at absolute positions Tk - Tq .. Tk - 1 against Tk keys
+// (flash-attention's bottom-right aligned causal mask); q / o are (B, Tq, ...),
+// k / v (B, Tk, ...), lse (B, Hq, Tq).
+static ttcd_status set_rows(ttcd::AttnArgs* a, int Tq, int Tk) {
+  if (Tq < 1 || Tq > Tk)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need 1 <= Tq <= Tk (got Tq=%d, Tk=%d)", Tq, Tk);
+  const int span = ttcd::wg_span_tokens(a->G);
+  a->q_off = Tk - Tq;
+  a->qb0 = a->q_off / span;
+  a->nqb = (Tk + span - 1) / span - a->qb0;
+  return TTCD_OK;
+}
+
+ttcd_status ttcd_dual_window_attn_kv_fwd(const void* q, const void* k, const void* v, void* o_t,
+                                         void* o_s, float* lse_t, float* lse_s, int B, int Tq,
+                                         int Tk, int Hq, int Hkv, int D,
+                                         const int64_t q_stride[4], const int64_t k_stride[4],
+                                         const int64_t v_stride[4], const int64_t o_stride[4],
+                                         int window_t, int window_s, float sm_scale,
+                                         ttcd_dtype dtype, void* stream) {
   ttcd_status st =
-      check_attn(q, k, v, o_t, B, T, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
+      check_attn(q, k, v, o_t, B, Tk, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
   if (st != TTCD_OK) return st;
   if (!o_s) return fail(TTCD_ERR_INVALID_ARGUMENT, "null student output pointer");
   if (!aligned16(o_s)) return fail(TTCD_ERR_UNSUPPORTED, "o_s must be 16-byte aligned");
-  if (window_t < 0) window_t = T;
+  if (window_t < 0) window_t = Tk;
   if (window_s < 1) return fail(TTCD_ERR_INVALID_ARGUMENT, "window_s must be >= 1 (got %d)", window_s);
   if (window_s > window_t)
     return fail(TTCD_ERR_INVALID_ARGUMENT, "window_s (%d) must be <= window_t (%d)", window_s,
                 window_t);
   if (!(sm_scale > 0.f) || !isfinite(sm_scale))
     return fail(TTCD_ERR_INVALID_ARGUMENT, "sm_scale must be finite and > 0");
-  ttcd::AttnArgs a = fill_args(q, k, v, B, T, Hq, Hkv, q_stride, k_stride, v_stride, o_stride,
+  ttcd::AttnArgs a = fill_args(q, k, v, B, Tk, Hq, Hkv, q_stride, k_stride, v_stride, o_stride,
                                sm_scale);
+  st = set_rows(&a, Tq, Tk);
+  if (st != TTCD_OK) return st;
   a.o_t = o_t;
   a.o_s = o_s;
   a.lse_t = lse_t;
   a.lse_s = lse_s;
-  a.sched = ttcd::make_dual_schedule(T, window_s, window_t);
+  a.sched = ttcd::make_dual_schedule(Tk, window_s, window_t);
   return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
                   "dual-window attention launch");
+}
+
+ttcd_status ttcd_dual_window_attn_fwd(const void* q, const void* k, const void* v, void* o_t,
+                                      void* o_s, float* lse_t, float* lse_s, int B, int T,
+                                      int Hq, int Hkv, int D, const int64_t q_stride[4],
+                                      const int64_t k_stride[4], const int64_t v_stride[4],
+                                      const int64_t o_stride[4], int window_t, int window_s,
+                                      float sm_scale, ttcd_dtype dtype, void* stream) {
+  return ttcd_dual_window_attn_kv_fwd(q, k, v, o_t, o_s, lse_t, lse_s, B, T, T, Hq, Hkv, D,
+                                      q_stride, k_stride, v_stride, o_stride, window_t, window_s,
+                                      sm_scale, dtype, stream);
+}
+
+ttcd_status ttcd_band_attn_kv_fwd(const void* q, const void* k, const void* v, void* o,
+                                  float* lse, int B, int Tq, int Tk, int Hq, int Hkv, int D,
+                                  const int64_t q_stride[4], const int64_t k_stride[4],
+                                  const int64_t v_stride[4], const int64_t o_stride[4],
+                                  int band_lo, int band_hi, float sm_scale, ttcd_dtype dtype,
+                                  void* stream) {
+  ttcd_status st =
+      check_attn(q, k, v, o, B, Tk, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
+  if (st != TTCD_OK) return st;
+  if (band_lo < 0 || band_hi <= band_lo)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi (got %d, %d)", band_lo,
+                band_hi);
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "sm_scale must be finite and > 0");
+  ttcd::AttnArgs a = fill_args(q, k, v, B, Tk, Hq, Hkv, q_stride, k_stride, v_stride, o_stride,
+                               sm_scale);
+  st = set_rows(&a, Tq, Tk);
+  if (st != TTCD_OK) return st;
+  a.o_t = o;
+  a.lse_t = lse;
+  a.sched = ttcd::make_band_schedule(Tk, band_lo, band_hi);
+  return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
+                  "band attention launch");
 }
 
 ttcd_status ttcd_band_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
@@ -154,21 +208,8 @@ ttcd_status ttcd_band_attn_fwd(const void* q, const void* k, const void* v, void
                                const int64_t k_stride[4], const int64_t v_stride[4],
                                const int64_t o_stride[4], int band_lo, int band_hi,
                                float sm_scale, ttcd_dtype dtype, void* stream) {
-  ttcd_status st =
-      check_attn(q, k, v, o, B, T, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
-  if (st != TTCD_OK) return st;
-  if (band_lo < 0 || band_hi <= band_lo)
-    return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi (got %d, %d)", band_lo,
-                band_hi);
-  if (!(sm_scale > 0.f) || !isfinite(sm_scale))
-    return fail(TTCD_ERR_INVALID_ARGUMENT, "sm_scale must be finite and > 0");
-  ttcd::AttnArgs a = fill_args(q, k, v, B, T, Hq, Hkv, q_stride, k_stride, v_stride, o_stride,
-                               sm_scale);
-  a.o_t = o;
-  a.lse_t = lse;
-  a.sched = ttcd::make_band_schedule(T, band_lo, band_hi);
-  return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
-                  "band attention launch");
+  return ttcd_band_attn_kv_fwd(q, k, v, o, lse, B, T, T, Hq, Hkv, D, q_stride, k_stride,
+                               v_stride, o_stride, band_lo, band_hi, sm_scale, dtype, stream);
 }
 
 ttcd_status ttcd_lse_merge_fwd(const void* o_s, const float* lse_s, const void* o_f,

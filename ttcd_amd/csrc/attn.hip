@@ -283,13 +283,13 @@ __device__ __forceinline__ float tile_max(const f32x16 (&s)[2]) {
 template <int D, typename T>
 __device__ __forceinline__ void emit(const f32x16 (&o)[Geo<D>::DT], float m, float l, float c,
                                      T* out, int64_t o_st, float* lse, int qrow, int T_,
-                                     int lane) {
+                                     int q_off, int lane) {
   using v4 = typename VecT<T>::v4;
   const float lt = xhalf_sum(l);
   const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-  if (qrow >= T_) return;
+  if (qrow >= T_ || qrow < q_off) return;  // rows of this launch only
   const int half = lane >> 5;
-  T* dst = out + (int64_t)qrow * o_st + half * 4;
+  T* dst = out + (int64_t)(qrow - q_off) * o_st + half * 4;
 #pragma unroll
   for (int dt = 0; dt < Geo<D>::DT; ++dt) {
 #pragma unroll
@@ -302,7 +302,7 @@ __device__ __forceinline__ void emit(const f32x16 (&o)[Geo<D>::DT], float m, flo
   }
   if (lse != nullptr && half == 0) {
     const float mc = (m == -INFINITY) ? 0.f : m * c;
-    lse[qrow] = lt > 0.f ? mc * 0.69314718055994531f + logf(lt) : -INFINITY;
+    lse[qrow - q_off] = lt > 0.f ? mc * 0.69314718055994531f + logf(lt) : -INFINITY;
   }
 }
 
@@ -508,7 +508,7 @@ void attn_fwd_kernel(AttnArgs a) {
   int rest = xcd_remap(__builtin_amdgcn_workgroup_id_x(), a.nwg);
   const int g = rest % a.G;
   rest /= a.G;
-  const int qb = a.nqb - 1 - rest % a.nqb;
+  const int qb = a.qb0 + (a.nqb - 1 - rest % a.nqb);
   rest /= a.nqb;
   const int hk = rest % a.Hkv;
   const int b = rest / a.Hkv;
@@ -516,7 +516,11 @@ void attn_fwd_kernel(AttnArgs a) {
   const int t0 = qb * kBlockM;
   const int r0 = __builtin_amdgcn_readfirstlane(t0 + wave * kWaveRows);
   const int t_last = min(t0 + kBlockM, T_) - 1;
-  const bool wave_valid = r0 < T_;
+  const int q_off = a.q_off;
+  const int Tq = T_ - q_off;
+  // a wave with no row in [q_off, T) computes nothing (it still takes part
+  // in the workgroup's loads and barriers)
+  const bool wave_valid = (r0 < T_) & (r0 + kWaveRows > q_off);
 
   const T* qp = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
   const T* kp = uniform_ptr(static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh);
@@ -531,11 +535,12 @@ void attn_fwd_kernel(AttnArgs a) {
   x.T_ = T_;
   x.ln = make_lane<D>(a.k_st, a.v_st, wave, lane);
   {
-    const T* src = qp + (int64_t)x.qrow * a.q_st + (lane >> 5) * 8;
+    const bool row_ok = (x.qrow < T_) & (x.qrow >= q_off);
+    const T* src = qp + (int64_t)(row_ok ? x.qrow - q_off : 0) * a.q_st + (lane >> 5) * 8;
 #pragma unroll
     for (int ks = 0; ks < G::DK; ++ks) {
       v8 z = {};
-      x.qf[ks] = x.qrow < T_ ? *reinterpret_cast<const v8*>(src + ks * 16) : z;
+      x.qf[ks] = row_ok ? *reinterpret_cast<const v8*>(src + ks * 16) : z;
     }
   }
 
@@ -668,8 +673,8 @@ void attn_fwd_kernel(AttnArgs a) {
     bool stored = false;
     if (DUAL && cur.act == kStudentLast) {
       T* os = static_cast<T*>(a.o_s) + b * a.o_sb + h * a.o_sh;
-      float* lse_s = a.lse_s ? a.lse_s + ((int64_t)b * a.Hq + h) * T_ : nullptr;
-      emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, lane);
+      float* lse_s = a.lse_s ? a.lse_s + ((int64_t)b * a.Hq + h) * Tq : nullptr;
+      emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, q_off, lane);
       emitted_s = true;
       stored = true;
     }
@@ -689,12 +694,12 @@ void attn_fwd_kernel(AttnArgs a) {
   if (wave_valid) {
     if (DUAL && !emitted_s) {
       T* os = static_cast<T*>(a.o_s) + b * a.o_sb + h * a.o_sh;
-      float* lse_s = a.lse_s ? a.lse_s + ((int64_t)b * a.Hq + h) * T_ : nullptr;
-      emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, lane);
+      float* lse_s = a.lse_s ? a.lse_s + ((int64_t)b * a.Hq + h) * Tq : nullptr;
+      emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, q_off, lane);
     }
     T* ot = static_cast<T*>(a.o_t) + b * a.o_sb + h * a.o_sh;
-    float* lse_t = a.lse_t ? a.lse_t + ((int64_t)b * a.Hq + h) * T_ : nullptr;
-    emit<D, T>(o, m, l, x.c, ot, a.o_st, lse_t, x.qrow, T_, lane);
+    float* lse_t = a.lse_t ? a.lse_t + ((int64_t)b * a.Hq + h) * Tq : nullptr;
+    emit<D, T>(o, m, l, x.c, ot, a.o_st, lse_t, x.qrow, T_, q_off, lane);
   }
 }
 

@@ -18,14 +18,17 @@ struct AttnArgs {
   const void* v;
   void* o_t;      // final output (teacher for the dual kernel, band output otherwise)
   void* o_s;      // student output (dual kernel only)
-  float* lse_t;   // optional (B, Hq, T)
-  float* lse_s;   // optional (B, Hq, T), dual kernel only
+  float* lse_t;   // optional (B, Hq, Tq)
+  float* lse_s;   // optional (B, Hq, Tq), dual kernel only
   int64_t q_sb, q_st, q_sh;
   int64_t k_sb, k_st, k_sh;
   int64_t v_sb, v_st, v_sh;
   int64_t o_sb, o_st, o_sh;
-  int B, T, Hq, Hkv, G;
-  int nqb;        // query tiles of kBlockM tokens per (b, h)
+  int B, T, Hq, Hkv, G;  // T: keys (Tk); query rows are absolute positions q_off..T-1
+  int q_off;      // Tk - Tq: absolute position of query row 0 (flash-attention's
+                  // bottom-right alignment; 0 when Tq == Tk)
+  int qb0;        // first query tile launched: q_off / kBlockM
+  int nqb;        // query tiles of kBlockM tokens per (b, h) launched
   int nwg;        // workgroups launched (set by the launcher)
   float c;        // sm_scale * log2(e)
   Schedule sched;
