@@ -16,8 +16,8 @@ kernel at w_T then w_S), one teacher-only call, the LSE-combination variant,
 the chunked causal conv at the reference's benchmark shape (GB/s vs 8 TB/s),
 the attention prologue (q/k RMSNorm + rotary) and epilogue (o_proj + dual
 residual RMSNorm) on the same layer, the batch / narrow-gap sweep (fused vs
-LSE variant), the ipttcdv9 prefill end to end (28 layers, T=32768, fused vs
-unfused), numerics at the CPU-runnable config, and the CPU baseline: the fp32 masked
+LSE variant), the ipttcdv9 prefill end to end (28 layers, T=32768; fused,
+patched and stock paths), numerics at the CPU-runnable config, and the CPU baseline: the fp32 masked
 softmax of the reference's CPU path (oracle restatement), query-chunked over
 the band, on a bounded sample of rows, on this host's cores.
 """
@@ -286,33 +286,38 @@ def sweep_measure(steps: int = 10, warmup: int = 2) -> list:
 E2E_T = 32768  # the e2e prefill length (config 5)
 
 
-def e2e_measure(steps: int = 5, warmup: int = 2, T: int = E2E_T, modes=(True, False)) -> dict:
+def e2e_measure(steps: int = 5, warmup: int = 2, T: int = E2E_T,
+                paths=("fused", "patched", "stock")) -> dict:
     """Prefill of the ipttcdv9 model at the Qwen3-0.6B shape (28 layers, TTT
     layers 0/7/14/21, w_T 8192, w_S 4096, conv K=5 on 3072 channels),
     random-init weights (the reference's init, seed 0), uniform token ids
-    (seed 1234), B=1, logits of the last token. Fused: the dual-window kernel,
-    the fused epilogue and the fused TTT feature pass; unfused: two windowed
-    calls, two o_proj GEMMs and separate SwiGLU / conv launches."""
+    (seed 1234), B=1, logits of the last token. Paths of the TTT layers:
+    "stock" = the reference's unpatched fast path (two windowed calls, torch's
+    conv); "patched" = its `--patch fused_conv` (one-pass dual-window kernel +
+    conv kernel); "fused" = patched + the fused epilogue and feature pass."""
     import torch
     from ttcd_amd import ipttcdv9
 
     dev = torch.device("cuda:0")
     cfg = ipttcdv9.QWEN3_06B_SWA8K
-    model = ipttcdv9.IPTTCDv9Prefill(cfg, ipttcdv9.init_weights(cfg, dev, seed=0))
+    weights = ipttcdv9.init_weights(cfg, dev, seed=0)
     g = torch.Generator(device=dev).manual_seed(1234)
     ids = torch.randint(0, cfg["vocab_size"], (1, T), device=dev, generator=g)
     flops = ipttcdv9.prefill_flops(cfg, 1, T)
     total = sum(flops.values())
     out = {"model": "ipttcdv9, Qwen3-0.6B shape (configs/ipttcd/ipttcdv9_qwen3_0.6B_ct_64k_v2_swa8k.json)",
            "B": 1, "T": T, "logits_to_keep": 1, "flops": flops}
-    for fused in modes:
-        ms = time_gpu(lambda: model.forward(ids, fused=fused), steps, warmup)
-        key = "fused" if fused else "unfused"
-        out[key] = {"ms": ms, "tokens_per_s": T / (ms * 1e-3),
-                    "tflops": total / (ms * 1e-3) / 1e12}
-        log(f"e2e prefill T={T} {key}: {ms:.2f} ms, {T / (ms * 1e-3):.0f} tok/s")
-    if "unfused" in out:
-        out["fused_speedup"] = out["unfused"]["ms"] / out["fused"]["ms"]
+    for path in paths:
+        model = ipttcdv9.IPTTCDv9Prefill(cfg, weights, path=path)
+        ms = time_gpu(lambda: model.forward(ids), steps, warmup)
+        out[path] = {"ms": ms, "tokens_per_s": T / (ms * 1e-3),
+                     "tflops": total / (ms * 1e-3) / 1e12}
+        log(f"e2e prefill T={T} {path}: {ms:.2f} ms, {T / (ms * 1e-3):.0f} tok/s")
+        del model
+    if "stock" in out:
+        out["fused_speedup_vs_stock"] = out["stock"]["ms"] / out["fused"]["ms"]
+    if "patched" in out:
+        out["fused_speedup_vs_patched"] = out["patched"]["ms"] / out["fused"]["ms"]
     out["peak_mem_gb"] = torch.cuda.max_memory_allocated(dev) / 1e9
     return out
 
@@ -385,7 +390,7 @@ def main() -> int:
     if args.only == "e2e":
         with torch.inference_mode():
             print(json.dumps({"only": "e2e", **e2e_measure(args.steps, args.warmup,
-                                                            modes=(True,))}), flush=True)
+                                                            paths=("fused",))}), flush=True)
         return 0
     if args.only == "sweep":
         with torch.inference_mode():

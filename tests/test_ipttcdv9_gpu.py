@@ -158,16 +158,32 @@ def test_prefill_matches_oracle(T):
     T=200: shorter than a chunk, so the TTT layers take the plain path."""
     c = M.resolve_config(TINY)
     w = M.init_weights(TINY, DEV, seed=0)
-    model = M.IPTTCDv9Prefill(TINY, w)
     ids = torch.randint(0, c["vocab_size"], (1, T), generator=torch.Generator().manual_seed(T))
-    got = model.forward(ids.to(DEV), logits_to_keep=8)
-    got2 = model.forward(ids.to(DEV), logits_to_keep=8, fused=False)
+    got = {p: M.IPTTCDv9Prefill(TINY, w, path=p).forward(ids.to(DEV), logits_to_keep=8)
+           for p in M.PATHS}
     torch.cuda.synchronize()
     want = R.prefill_ref(c, {k: v.cpu() for k, v in w.items()}, ids, 8, torch.bfloat16)
-    _logits_close(got, want)
-    _logits_close(got2, want)
-    # the fused kernels change only rounding
-    _logits_close(got, got2, max_frac=2e-2, mean_frac=1e-2)
+    for p in M.PATHS:
+        _logits_close(got[p], want)
+    # the patches change only rounding
+    _logits_close(got["fused"], got["stock"], max_frac=2e-2, mean_frac=1e-2)
+    _logits_close(got["fused"], got["patched"], max_frac=2e-2, mean_frac=1e-2)
+
+
+def test_patch_hooks_turn_stock_into_patched():
+    w = M.init_weights(TINY, DEV, seed=3)
+    model = M.IPTTCDv9Prefill(TINY, w, path="stock")
+    assert model.path == "stock"
+    assert M.patch_fused_attn(model) == 2 and M.patch_triton_conv(model) == 2
+    assert model.path == "patched"
+    ids = torch.randint(0, 1024, (1, 768), generator=torch.Generator().manual_seed(11)).to(DEV)
+    a = model.forward(ids, logits_to_keep=4)
+    b = M.IPTTCDv9Prefill(TINY, w, path="patched").forward(ids, logits_to_keep=4)
+    M.patch_fused_attn(model, kernel="fa3_lse")
+    lse = model.forward(ids, logits_to_keep=4)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    _logits_close(lse, a, max_frac=2e-2, mean_frac=1e-2)
 
 
 # SmolLM2-360M's attention shape (configs/ipttcd/ipttcdv9_smollm2_360M_ct_64k_v2_swa8k.json):

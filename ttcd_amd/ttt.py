@@ -155,8 +155,20 @@ class TttMlpWeights:
         self.conv_t, self.conv_s, self.b_proj = conv_t, conv_s, b_proj
 
 
+def stock_conv(v: torch.Tensor, cw: torch.Tensor) -> torch.Tensor:
+    """The reference's unpatched chunk-local conv (IPTTCDMLP._apply_ttt_conv,
+    modeling_ipttcdv9.py:203-211): (b, t, c, d) -> ((b t), d, c), left pad
+    K-1, torch's depthwise conv1d (MIOpen), back. The A/B baseline of the conv
+    kernel; its accumulation order is MIOpen's, not fixed."""
+    b, t, c, d = v.shape
+    K = cw.shape[-1]
+    xf = F.pad(v.permute(0, 1, 3, 2).reshape(b * t, d, c), (K - 1, 0))
+    y = F.conv1d(xf, cw.reshape(d, 1, K), groups=d)
+    return y.reshape(b, t, d, c).permute(0, 1, 3, 2).contiguous()
+
+
 def ttt_mlp(x: torch.Tensor, t: torch.Tensor, w: TttMlpWeights, *, chunk: int, lr: float,
-            update_every: int, fused: bool = True) -> torch.Tensor:
+            update_every: int, fused: bool = True, conv: str = "kernel") -> torch.Tensor:
     """The TTT MLP forward for a prefill: x the teacher hidden states after
     mlp_norm, t the student's (B, L, H). Returns the MLP output (B, L, H).
 
@@ -169,7 +181,9 @@ def ttt_mlp(x: torch.Tensor, t: torch.Tensor, w: TttMlpWeights, *, chunk: int, l
         y_c     = z_c @ W_c^T
     with W_cur = W_down for the first group and advanced by the group's last
     cumsum at its end. `fused=False` runs the feature pass as separate launches
-    (swiglu, conv, subtraction) for A/B measurement; results are identical."""
+    (swiglu, conv, subtraction) for A/B measurement, with the conv kernel
+    (conv="kernel": identical results) or the reference's unpatched torch
+    conv (conv="stock")."""
     from .conv import causal_dwconv_x
 
     B, L, H = x.shape
@@ -184,19 +198,23 @@ def ttt_mlp(x: torch.Tensor, t: torch.Tensor, w: TttMlpWeights, *, chunk: int, l
     rows = B * nchunk * C
     gu = F.linear(_stack_rows(x, t), w.gate_up)  # one GEMM over teacher and student rows
     gu_t, gu_s = gu[:rows], gu[rows:]
-    if fused:
+    if conv not in ("kernel", "stock"):
+        raise ValueError(f"ttt_mlp: conv must be 'kernel' or 'stock', got {conv!r}")
+    if fused and conv == "kernel":
         z, z_hat, diff = ttt_features(gu_t, gu_s, w.conv_t, w.conv_s, B, nchunk, C)
     else:
         z = swiglu(gu_t[:, :I], gu_t[:, I:])
         z_raw = swiglu(gu_s[:, :I], gu_s[:, I:])
 
-        def conv(v, cw):
+        def apply_conv(v, cw):
             if cw is None:
                 return v
+            if conv == "stock":
+                return stock_conv(v.view(B, nchunk, C, I), cw).view(rows, I)
             return causal_dwconv_x(v.view(B * nchunk, C, I), cw.reshape(I, -1)).view(rows, I)
 
-        z_tgt = conv(z, w.conv_t)
-        z_hat = conv(z_raw, w.conv_s)
+        z_tgt = apply_conv(z, w.conv_t)
+        z_hat = apply_conv(z_raw, w.conv_s)
         keep = torch.arange(nchunk, device=dev) < nchunk - 1
         diff = (z_tgt.view(B, nchunk, C, I)[:, keep] - z_hat.view(B, nchunk, C, I)[:, keep])
         diff = diff.reshape(-1, I)
