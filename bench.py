@@ -55,11 +55,19 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_gpu(fn, steps: int, warmup: int) -> float:
-    """Mean ms per call over `steps` calls, HIP events on the current (launch) stream."""
+def time_gpu(fn, steps: int, warmup: int, min_warm_s: float = 0.2) -> float:
+    """Mean ms per call over `steps` calls, HIP events on the current (launch) stream.
+    Warm-up is `warmup` calls and at least `min_warm_s` of back-to-back work: a
+    short kernel timed right after the GPU idled runs up to 18 % slow (measured
+    for the 1 ms B=1, T=16384 sweep point) while the clocks ramp."""
     import torch
-    for _ in range(warmup):
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < min_warm_s:
         fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
