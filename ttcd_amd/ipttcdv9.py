@@ -40,7 +40,6 @@ reference's cache writes are copies of k and v).
 """
 from __future__ import annotations
 
-import math
 
 import torch
 import torch.nn.functional as F

@@ -42,19 +42,17 @@ def _check_gpu(fn: str, **tensors):
 
 
 def _row_stride(t: torch.Tensor, fn: str, name: str) -> int:
+    """Element stride between consecutive rows of t seen as (rows, t.shape[-1]):
+    the last dim must be contiguous and the leading dims evenly strided (a
+    contiguous tensor, or a column slice of one, such as half of a GEMM output)."""
     if t.dim() < 1 or t.stride(-1) != 1:
         raise ValueError(f"{fn}: {name} must have a contiguous last dim")
-    rows_shape = t.shape[:-1]
-    if len(rows_shape) == 0:
-        return t.shape[-1]
-    # rows must be evenly strided (a 2-D view of the leading dims)
-    flat = t.reshape(-1, t.shape[-1]) if t.is_contiguous() else None
-    if flat is not None:
+    if t.dim() == 1 or t.is_contiguous():
         return t.shape[-1]
     st = t.stride(-2)
     expect = st
     for d in range(t.dim() - 2, -1, -1):
-        if t.stride(d) != expect:
+        if t.shape[d] != 1 and t.stride(d) != expect:
             raise ValueError(f"{fn}: {name} rows must be evenly strided")
         expect *= t.shape[d]
     return st
