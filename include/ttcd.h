@@ -214,6 +214,19 @@ ttcd_status ttcd_rmsnorm_fwd(const void* x, const void* residual,
                              int hidden, ttcd_dtype dtype, void* stream);
 
 /*
+ * The block's closing residual add fused with the next block's plain RMSNorm
+ * (custom_models/ipttcd/modeling_ipttcdv9.py:870 `hidden_states = residual +
+ * hidden_states`, a bf16 torch add, then :627 `self.attn_norm(...)`):
+ * sum_out = f32(x) + f32(residual) rounded to dtype, y = RMSNorm(sum_out) * w
+ * computed from the ROUNDED sum, exactly as the two separate launches.
+ * Numerics, layout and limits as ttcd_rmsnorm_fwd.
+ */
+ttcd_status ttcd_add_rmsnorm_fwd(const void* x, const void* residual,
+                                 const void* norm_w, ttcd_dtype w_dtype,
+                                 float eps, void* y, void* sum_out, int64_t rows,
+                                 int hidden, ttcd_dtype dtype, void* stream);
+
+/*
  * SwiGLU, fla's swiglu_fwd (fla/modules/activations.py:412-471, used by
  * swiglu and swiglu_linear in every MLP of the model): out = (g * s) * u
  * with s = 1 / (1 + exp(-g)), in fp32, rounded to dtype. Row-strided

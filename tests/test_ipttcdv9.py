@@ -236,6 +236,19 @@ def test_rmsnorm_abi_rejects():
     assert call(rows=0) == _lib.TTCD_OK
 
 
+def test_add_rmsnorm_abi_rejects():
+    L = _lib.lib()
+    args = [_P, _P, _P, _lib.DTYPE_BF16, 1e-6, _P, _P, 4, 64, _lib.DTYPE_BF16, None]
+    bad = list(args); bad[1] = None
+    assert L.ttcd_add_rmsnorm_fwd(*bad) == _lib.TTCD_ERR_INVALID_ARGUMENT
+    bad = list(args); bad[8] = 2056
+    assert L.ttcd_add_rmsnorm_fwd(*bad) == _lib.TTCD_ERR_UNSUPPORTED
+    bad = list(args); bad[6] = ctypes.c_void_p(0x10008)
+    assert L.ttcd_add_rmsnorm_fwd(*bad) == _lib.TTCD_ERR_UNSUPPORTED
+    ok = list(args); ok[7] = 0
+    assert L.ttcd_add_rmsnorm_fwd(*ok) == _lib.TTCD_OK
+
+
 def test_swiglu_abi_rejects():
     L = _lib.lib()
     assert L.ttcd_swiglu_fwd(None, _P, _P, 4, 64, 64, 64, 64, _lib.DTYPE_BF16, None) == \

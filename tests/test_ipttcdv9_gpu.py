@@ -46,6 +46,19 @@ def test_rmsnorm_matches_oracle(H, res, wdt):
     _ulp_ok(y, ry)
 
 
+def test_add_rmsnorm_is_the_add_then_the_norm():
+    # a bf16 torch add, then fla's RMSNorm of the rounded sum
+    x = _rand(2, 333, 1024, seed=11)
+    r = _rand(2, 333, 1024, seed=12, scale=4.0)
+    w = (1 + 0.2 * _rand(1024, seed=13, dtype=torch.float32)).to(torch.bfloat16)
+    with torch.inference_mode():
+        y, h = epilogue.add_rmsnorm(x.to(DEV), r.to(DEV), w.to(DEV), 1e-6)
+        want_h = r.to(DEV) + x.to(DEV)
+    torch.cuda.synchronize()
+    assert torch.equal(h, want_h)
+    _ulp_ok(y, prologue_ref.rms_norm_ref(want_h.cpu(), w, 1e-6))
+
+
 def test_swiglu_matches_oracle_on_strided_halves():
     gu = _rand(777, 2 * 3072, seed=4, scale=2.0)
     with torch.inference_mode():

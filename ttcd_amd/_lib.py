@@ -39,6 +39,7 @@ EXPORTS = (
     "ttcd_rope_table_fwd",
     "ttcd_dual_residual_rmsnorm_fwd",
     "ttcd_rmsnorm_fwd",
+    "ttcd_add_rmsnorm_fwd",
     "ttcd_swiglu_fwd",
     "ttcd_ttt_features_fwd",
     "ttcd_attn_schedule_coverage",
@@ -87,6 +88,8 @@ _SIGS = {
     "ttcd_dual_residual_rmsnorm_fwd": (_i32, [
         _vp, _vp, _vp, _vp, _i32, ctypes.c_float, _vp, _vp, _vp, _i64, _i32, _i32, _vp]),
     "ttcd_rmsnorm_fwd": (_i32, [
+        _vp, _vp, _vp, _i32, ctypes.c_float, _vp, _vp, _i64, _i32, _i32, _vp]),
+    "ttcd_add_rmsnorm_fwd": (_i32, [
         _vp, _vp, _vp, _i32, ctypes.c_float, _vp, _vp, _i64, _i32, _i32, _vp]),
     "ttcd_swiglu_fwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i32, _vp]),
     "ttcd_ttt_features_fwd": (_i32, [

@@ -403,6 +403,35 @@ ttcd_status ttcd_rmsnorm_fwd(const void* x, const void* residual, const void* no
                   "rmsnorm launch");
 }
 
+ttcd_status ttcd_add_rmsnorm_fwd(const void* x, const void* residual, const void* norm_w,
+                                 ttcd_dtype w_dtype, float eps, void* y, void* sum_out,
+                                 int64_t rows, int hidden, ttcd_dtype dtype, void* stream) {
+  if (!x || !residual || !norm_w || !y || !sum_out)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (rows < 0 || hidden < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need rows >= 0 and hidden >= 1");
+  if (hidden % 8 != 0 || hidden > 2048)
+    return fail(TTCD_ERR_UNSUPPORTED, "hidden size %d not supported (a multiple of 8, <= 2048)",
+                hidden);
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "activation dtype must be bf16 or f16");
+  if ((unsigned)w_dtype > TTCD_DTYPE_F32)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "unknown norm weight dtype");
+  if (!(eps >= 0.f) || !isfinite(eps))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+  const void* all[4] = {x, residual, y, sum_out};
+  for (int i = 0; i < 4; ++i)
+    if (!aligned16(all[i]))
+      return fail(TTCD_ERR_UNSUPPORTED, "tensor base pointers must be 16-byte aligned");
+  if (w_dtype != TTCD_DTYPE_F32 && !aligned16(norm_w))
+    return fail(TTCD_ERR_UNSUPPORTED, "16-bit norm weights must be 16-byte aligned");
+  if (rows == 0) return ok();
+  return from_hip(ttcd::launch_dual_residual_rmsnorm(
+                      x, nullptr, residual, norm_w, elem(w_dtype), eps, y, sum_out, nullptr,
+                      rows, hidden, elem(dtype), static_cast<hipStream_t>(stream), true),
+                  "add rmsnorm launch");
+}
+
 ttcd_status ttcd_swiglu_fwd(const void* gate, const void* up, void* out, int64_t rows, int cols,
                             int64_t gate_stride, int64_t up_stride, int64_t out_stride,
                             ttcd_dtype dtype, void* stream) {

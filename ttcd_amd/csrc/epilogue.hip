@@ -18,9 +18,11 @@
 //
 // The same kernel, with one branch, is the model's other RMSNorms: the
 // residual prenorm after a plain attention layer
-// (custom_models/ipttcd/modeling_ipttcdv9.py:863) and the plain RMSNorm of
+// (custom_models/ipttcd/modeling_ipttcdv9.py:863), the plain RMSNorm of
 // attn_norm and of the final norm (:627, :1112; layernorm.py:189-251
-// without a residual).
+// without a residual), and the block's closing residual add (:870, a bf16
+// torch add) fused with the next block's attn_norm: the sum is stored
+// rounded and normalised from its rounded value, as the two launches do.
 //
 // One wavefront per row: lane l owns the 16-byte chunks l, l + 64, ... of
 // the row, so every access is a coalesced 1 KiB transaction.
@@ -58,8 +60,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 // MAXC: 16-byte chunks per lane (H <= 512 * MAXC; the fp32 sums stay in
 // registers between the two passes, so H <= 2048). DUAL: a second (student)
 // branch on the same residual. RES: a residual is added (prenorm form, with
-// residual_out); without it the kernel is fla's plain RMSNorm of a.
-template <typename T, typename W, int MAXC, bool DUAL, bool RES>
+// residual_out); without it the kernel is fla's plain RMSNorm of a. RND: the
+// sum is rounded to T before the norm (a torch add, then the next RMSNorm).
+template <typename T, typename W, int MAXC, bool DUAL, bool RES, bool RND = false>
 __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(
     const T* __restrict__ a_t, const T* __restrict__ a_s, const T* __restrict__ res,
     const W* __restrict__ w, float eps, T* __restrict__ y_t, T* __restrict__ res_out,
@@ -87,6 +90,7 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(
     for (int e = 0; e < 8; ++e) {
       const float r = RES ? static_cast<float>(vr.e[e]) : 0.f;
       xt[c][e] = RES ? static_cast<float>(vt.e[e]) + r : static_cast<float>(vt.e[e]);
+      if (RND) xt[c][e] = static_cast<float>(round_to<T>(xt[c][e]));
       if (DUAL) xs[c][e] = static_cast<float>(vs.e[e]) + r;
       if (RES) ro.e[e] = round_to<T>(xt[c][e]);
       sst = fmaf(xt[c][e], xt[c][e], sst);
@@ -125,7 +129,8 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(
 
 template <typename T, typename W, int MAXC>
 hipError_t launch_c(const void* a_t, const void* a_s, const void* res, const void* w, float eps,
-                    void* y_t, void* res_out, void* y_s, int64_t rows, int H, hipStream_t st) {
+                    void* y_t, void* res_out, void* y_s, int64_t rows, int H, bool rnd,
+                    hipStream_t st) {
   const int64_t blocks = (rows + 3) / 4;
   const bool dual = a_s != nullptr, has_res = res != nullptr;
   auto go = [&](auto kern) {
@@ -137,6 +142,8 @@ hipError_t launch_c(const void* a_t, const void* a_s, const void* res, const voi
   };
   if (dual) {
     go(residual_rmsnorm_kernel<T, W, MAXC, true, true>);  // dual always has a residual
+  } else if (has_res && rnd) {
+    go(residual_rmsnorm_kernel<T, W, MAXC, false, true, true>);
   } else if (has_res) {
     go(residual_rmsnorm_kernel<T, W, MAXC, false, true>);
   } else {
@@ -147,21 +154,27 @@ hipError_t launch_c(const void* a_t, const void* a_s, const void* res, const voi
 
 template <typename T, typename W>
 hipError_t launch_h(const void* a_t, const void* a_s, const void* res, const void* w, float eps,
-                    void* y_t, void* res_out, void* y_s, int64_t rows, int H, hipStream_t st) {
+                    void* y_t, void* res_out, void* y_s, int64_t rows, int H, bool rnd,
+                    hipStream_t st) {
   const int nch = H / 8;
-  if (nch <= 64) return launch_c<T, W, 1>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
-  if (nch <= 128) return launch_c<T, W, 2>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
-  return launch_c<T, W, 4>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
+  if (nch <= 64)
+    return launch_c<T, W, 1>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, rnd, st);
+  if (nch <= 128)
+    return launch_c<T, W, 2>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, rnd, st);
+  return launch_c<T, W, 4>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, rnd, st);
 }
 
 template <typename T>
 hipError_t launch_w(const void* a_t, const void* a_s, const void* res, const void* w, Elem wt,
-                    float eps, void* y_t, void* res_out, void* y_s, int64_t rows, int H,
+                    float eps, void* y_t, void* res_out, void* y_s, int64_t rows, int H, bool rnd,
                     hipStream_t st) {
   switch (wt) {
-    case Elem::BF16: return launch_h<T, __bf16>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
-    case Elem::F16: return launch_h<T, _Float16>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
-    default: return launch_h<T, float>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, st);
+    case Elem::BF16:
+      return launch_h<T, __bf16>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, rnd, st);
+    case Elem::F16:
+      return launch_h<T, _Float16>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, rnd, st);
+    default:
+      return launch_h<T, float>(a_t, a_s, res, w, eps, y_t, res_out, y_s, rows, H, rnd, st);
   }
 }
 
@@ -170,10 +183,11 @@ hipError_t launch_w(const void* a_t, const void* a_s, const void* res, const voi
 hipError_t launch_dual_residual_rmsnorm(const void* a_t, const void* a_s, const void* res,
                                         const void* w, Elem wt, float eps, void* y_t,
                                         void* res_out, void* y_s, int64_t rows, int H,
-                                        Elem dtype, hipStream_t stream) {
-  return dtype == Elem::BF16
-             ? launch_w<__bf16>(a_t, a_s, res, w, wt, eps, y_t, res_out, y_s, rows, H, stream)
-             : launch_w<_Float16>(a_t, a_s, res, w, wt, eps, y_t, res_out, y_s, rows, H, stream);
+                                        Elem dtype, hipStream_t stream, bool round_sum) {
+  return dtype == Elem::BF16 ? launch_w<__bf16>(a_t, a_s, res, w, wt, eps, y_t, res_out, y_s,
+                                                rows, H, round_sum, stream)
+                             : launch_w<_Float16>(a_t, a_s, res, w, wt, eps, y_t, res_out, y_s,
+                                                  rows, H, round_sum, stream);
 }
 
 }  // namespace ttcd

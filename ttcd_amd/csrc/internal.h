@@ -66,7 +66,7 @@ hipError_t launch_rope_table(void* cos_t, void* sin_t, const float* inv_freq, in
 hipError_t launch_dual_residual_rmsnorm(const void* a_t, const void* a_s, const void* res,
                                         const void* w, Elem wt, float eps, void* y_t,
                                         void* res_out, void* y_s, int64_t rows, int H,
-                                        Elem dtype, hipStream_t stream);
+                                        Elem dtype, hipStream_t stream, bool round_sum = false);
 
 // TTT MLP feature pass (ttt.hip). Rows are b-major, then chunk, then position.
 struct TttFeatureArgs {

@@ -18,6 +18,9 @@ twice and also store the student's discarded residual sum), with one GEMM
         -> (hidden_states, residual_out, student_output)
     rmsnorm(x, weight, eps, residual=None)
         -> y, or (y, x + residual) with a residual (the model's other norms)
+    add_rmsnorm(x, residual, weight, eps)
+        -> (RMSNorm(h), h = residual + x rounded): a block's closing add + the
+        next block's attn_norm
     fused_attn_epilogue(o_proj, mlp_norm, o_t, o_s, residual)
         drop-in for the call site above
 """
@@ -110,6 +113,33 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
             res_out.data_ptr() if res_out is not None else None, rows, H, _DT[x.dtype],
             torch.cuda.current_stream(x.device).cuda_stream))
     return y if res is None else (y, res_out)
+
+
+def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """``h = residual + x`` (a bf16/f16 torch add) followed by fla's plain
+    RMSNorm of h, in one pass: returns (RMSNorm(h) * weight, h), with the norm
+    taken on the ROUNDED h as the two separate launches take it
+    (custom_models/ipttcd/modeling_ipttcdv9.py:870, then :627 of the next
+    block)."""
+    for name, t in (("x", x), ("residual", residual), ("weight", weight)):
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise ValueError(f"add_rmsnorm: {name} must be a tensor on a GPU (HIP) device")
+    if x.dtype not in (torch.bfloat16, torch.float16) or residual.dtype != x.dtype \
+            or residual.shape != x.shape:
+        raise ValueError("add_rmsnorm: x and residual must match in shape and bf16/f16 dtype")
+    H = x.shape[-1]
+    if weight.shape != (H,) or weight.dtype not in _DT:
+        raise ValueError(f"add_rmsnorm: weight must be ({H},) of bf16, f16 or f32")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, residual, weight)):
+        raise RuntimeError("add_rmsnorm is forward-only: call it under torch.no_grad()")
+    x, res, w = x.contiguous(), residual.contiguous(), weight.contiguous()
+    y, h = torch.empty_like(x), torch.empty_like(x)
+    rows = x.numel() // H if H > 0 else 0
+    if rows > 0:
+        _lib.check(_lib.lib().ttcd_add_rmsnorm_fwd(
+            x.data_ptr(), res.data_ptr(), w.data_ptr(), _DT[w.dtype], float(eps), y.data_ptr(),
+            h.data_ptr(), rows, H, _DT[x.dtype], torch.cuda.current_stream(x.device).cuda_stream))
+    return y, h
 
 
 def _stacked(o_t: torch.Tensor, o_s: torch.Tensor) -> torch.Tensor:

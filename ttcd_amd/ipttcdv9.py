@@ -13,7 +13,8 @@ hipBLASLt GEMM through torch.
 Per layer (attn_norm = fla RMSNorm; qk_norm + rotary; window W_T):
   plain layer: h -> RMSNorm -> one q|k|v GEMM -> q/k RMSNorm + rotary (one
       kernel) -> band attention (window W_T) -> o_proj -> residual RMSNorm
-      -> gate|up GEMM -> SwiGLU -> down GEMM -> residual add
+      -> gate|up GEMM -> SwiGLU -> down GEMM -> residual add (one kernel with
+      the next block's RMSNorm, the sum rounded first as the reference's add)
   TTT layer:   ... -> fused dual-window attention (W_T, W_S = visible chunks
       x ttt_chunk) -> one o_proj GEMM over both outputs -> dual residual
       RMSNorm -> TTT MLP (ttcd_amd.ttt.ttt_mlp) -> residual add
@@ -261,13 +262,19 @@ class IPTTCDv9Prefill:
         return (_attn.window_attn(q, k, v, self.window_t),
                 _attn.window_attn(q, k, v, self.window_s))
 
-    def layer(self, i: int, h: torch.Tensor) -> torch.Tensor:
+    def layer(self, i: int, h: torch.Tensor, y_prev: torch.Tensor | None = None):
+        """One block. With y_prev, the block input is h + y_prev (the previous
+        block's closing residual add), fused with this block's attn_norm.
+        Returns (residual, y): the block output is residual + y."""
         c, w = self.cfg, self.w
         p = f"model.layers.{i}."
         eps = c["norm_eps"]
         B, T, H = h.shape
-        residual = h
-        x = _epi.rmsnorm(h, w[p + "attn_norm.weight"], eps)
+        if y_prev is None:
+            residual = h
+            x = _epi.rmsnorm(h, w[p + "attn_norm.weight"], eps)
+        else:
+            x, residual = _epi.add_rmsnorm(y_prev, h, w[p + "attn_norm.weight"], eps)
         q, k, v = self._qkv(i, x)
         o_w = w[p + "attn.o_proj.weight"]
         if i in self.ttt and T >= c["ttt_chunk"]:
@@ -289,7 +296,7 @@ class IPTTCDv9Prefill:
             a = F.linear(o.reshape(B, T, -1), o_w)
             x, residual = _epi.rmsnorm(a, w[p + "mlp_norm.weight"], eps, residual=residual)
             y = _ttt.swiglu_mlp(x, self.gu_w[i], w[p + "mlp.down_proj.weight"])
-        return residual + y
+        return residual, y
 
     @torch.inference_mode()
     def forward(self, input_ids: torch.Tensor, logits_to_keep: int = 1) -> torch.Tensor:
@@ -299,9 +306,12 @@ class IPTTCDv9Prefill:
         if input_ids.dim() != 2 or input_ids.device != self.dev:
             raise ValueError("input_ids must be (B, T) on the model's device")
         h = F.embedding(input_ids, self.w["model.embeddings.weight"])
+        y = None
         for i in range(self.cfg["num_hidden_layers"]):
-            h = self.layer(i, h)
-        keep = h[:, -logits_to_keep:] if logits_to_keep > 0 else h
+            h, y = self.layer(i, h, y)
+        if logits_to_keep > 0:  # only the kept rows of the last block's output
+            h, y = h[:, -logits_to_keep:], y[:, -logits_to_keep:]
+        keep = h + y
         x = _epi.rmsnorm(keep.contiguous(), self.w["model.norm.weight"], self.cfg["norm_eps"])
         return F.linear(x, self.w["lm_head.weight"])
 
