@@ -108,6 +108,42 @@ ttcd_status ttcd_band_attn_kv_fwd(
     ttcd_dtype dtype, void* stream);
 
 /*
+ * Packed variable-length sequences (flash-attention's varlen layout): the
+ * same two calls on nseq sequences packed along the token axis. Sequence b
+ * is rows cu_seqlens[b] .. cu_seqlens[b+1]-1 of q, k, v and the outputs;
+ * every sequence is its own causal prefill (queries == keys). Replaces the
+ * flash_attn_varlen_func(cu_seqlens_q=cu_seqlens, cu_seqlens_k=cu_seqlens,
+ * ..., causal=True, window_size=(W-1, 0)) calls of the packed-batch path
+ * (fla/layers/attn.py:255-270), which the reference's fused prefill declines
+ * (_use_fast_prefill_path returns False for cu_seqlens,
+ * custom_models/ipttcd/modeling_ipttcdv9.py:570-571).
+ *   q, o_t, o_s, o: (total, Hq, D); k, v: (total, Hkv, D); strides are the
+ *   token, head and d strides (d-stride 1). lse*: (Hq, total) fp32.
+ *   cu_seqlens: device int32[nseq + 1], nondecreasing, cu_seqlens[0] = 0,
+ *   cu_seqlens[nseq] = total. It is read on the device (no host sync); each
+ *   sequence is clamped to rows [0, total) and to max_seqlen rows, so
+ *   malformed offsets cannot cause an out-of-bounds access. Rows outside
+ *   every sequence are not written.
+ *   max_seqlen: the longest sequence (sizes the grid).
+ * Windows, bands and every other argument as in the fixed-length calls
+ * (window_t < 0: full causal within each sequence).
+ */
+ttcd_status ttcd_dual_window_attn_varlen_fwd(
+    const void* q, const void* k, const void* v, void* o_t, void* o_s,
+    float* lse_t, float* lse_s, const int32_t* cu_seqlens, int nseq,
+    int max_seqlen, int total, int Hq, int Hkv, int D,
+    const int64_t q_stride[3], const int64_t k_stride[3],
+    const int64_t v_stride[3], const int64_t o_stride[3], int window_t,
+    int window_s, float sm_scale, ttcd_dtype dtype, void* stream);
+
+ttcd_status ttcd_band_attn_varlen_fwd(
+    const void* q, const void* k, const void* v, void* o, float* lse,
+    const int32_t* cu_seqlens, int nseq, int max_seqlen, int total, int Hq,
+    int Hkv, int D, const int64_t q_stride[3], const int64_t k_stride[3],
+    const int64_t v_stride[3], const int64_t o_stride[3], int band_lo,
+    int band_hi, float sm_scale, ttcd_dtype dtype, void* stream);
+
+/*
  * Exact log-sum-exp merge of two attention partials over disjoint key sets.
  * Replaces _lse_merge_kernel + the o_t[:, :WS] copy of
  * lse_dual_window_attn_fa3_fast (profiling/lse_dual_attn.py:106-131, :151-159).

@@ -100,3 +100,45 @@ def test_merge_rejects():
     assert lib.ttcd_lse_merge_fwd(p, p, p, p, None, 1, 64, 4, 64, 0, st, 0, None) == 1
     assert lib.ttcd_lse_merge_fwd(p, p, p, p, p, 1, 64, 4, 12, 0, st, 0, None) == 2
     assert lib.ttcd_lse_merge_fwd(p, p, p, p, p, 1, 64, 4, 64, -1, st, 0, None) == 1
+
+
+def _varlen_call(fn="dual", **over):
+    """Varlen entry points with fake (never dereferenced) 16-byte aligned pointers."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x10000)
+    args = dict(cu=p, nseq=2, max_seqlen=64, total=100, Hq=4, Hkv=2, D=64, wt=32, ws=16,
+                lo=0, hi=32, scale=0.125, dtype=_lib.DTYPE_BF16, q=p,
+                qs=_lib.strides3([4 * 64, 64, 1]), ks=_lib.strides3([2 * 64, 64, 1]))
+    args.update(over)
+    common = (args["cu"], args["nseq"], args["max_seqlen"], args["total"], args["Hq"],
+              args["Hkv"], args["D"], args["qs"], args["ks"], args["ks"], args["qs"])
+    if fn == "dual":
+        return lib.ttcd_dual_window_attn_varlen_fwd(
+            args["q"], p, p, p, p, None, None, *common, args["wt"], args["ws"], args["scale"],
+            args["dtype"], None)
+    return lib.ttcd_band_attn_varlen_fwd(
+        args["q"], p, p, p, None, *common, args["lo"], args["hi"], args["scale"], args["dtype"],
+        None)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(cu=None), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(nseq=0), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(max_seqlen=0), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(total=-1), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(ws=0), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(ws=33), _lib.TTCD_ERR_INVALID_ARGUMENT),           # ws > wt
+    (dict(D=96), _lib.TTCD_ERR_UNSUPPORTED),
+    (dict(Hq=3), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(q=ctypes.c_void_p(0x10008)), _lib.TTCD_ERR_UNSUPPORTED),
+    (dict(qs=_lib.strides3([4 * 64, 64, 2])), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(scale=float("inf")), _lib.TTCD_ERR_INVALID_ARGUMENT),
+])
+def test_dual_varlen_rejects(over, status):
+    assert _varlen_call("dual", **over) == status
+    assert _lib.lib().ttcd_last_error()
+
+
+@pytest.mark.parametrize("lo,hi", [(-1, 4), (5, 5), (7, 3)])
+def test_band_varlen_rejects(lo, hi):
+    assert _varlen_call("band", lo=lo, hi=hi) == _lib.TTCD_ERR_INVALID_ARGUMENT

@@ -33,6 +33,8 @@ EXPORTS = (
     "ttcd_band_attn_fwd",
     "ttcd_dual_window_attn_kv_fwd",
     "ttcd_band_attn_kv_fwd",
+    "ttcd_dual_window_attn_varlen_fwd",
+    "ttcd_band_attn_varlen_fwd",
     "ttcd_lse_merge_fwd",
     "ttcd_causal_dwconv_chunked_fwd",
     "ttcd_qk_norm_rope_fwd",
@@ -50,6 +52,7 @@ _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
 _fp = ctypes.c_void_p  # float* passed as a raw address
 _i64x4 = ctypes.POINTER(ctypes.c_int64)
+_i64x3 = ctypes.POINTER(ctypes.c_int64)
 
 _SIGS = {
     "ttcd_status_string": (ctypes.c_char_p, [_i32]),
@@ -74,6 +77,16 @@ _SIGS = {
         _vp, _vp, _vp, _vp, _fp,
         _i32, _i32, _i32, _i32, _i32, _i32,
         _i64x4, _i64x4, _i64x4, _i64x4,
+        _i32, _i32, ctypes.c_float, _i32, _vp]),
+    "ttcd_dual_window_attn_varlen_fwd": (_i32, [
+        _vp, _vp, _vp, _vp, _vp, _fp, _fp, _vp,
+        _i32, _i32, _i32, _i32, _i32, _i32,
+        _i64x3, _i64x3, _i64x3, _i64x3,
+        _i32, _i32, ctypes.c_float, _i32, _vp]),
+    "ttcd_band_attn_varlen_fwd": (_i32, [
+        _vp, _vp, _vp, _vp, _fp, _vp,
+        _i32, _i32, _i32, _i32, _i32, _i32,
+        _i64x3, _i64x3, _i64x3, _i64x3,
         _i32, _i32, ctypes.c_float, _i32, _vp]),
     "ttcd_lse_merge_fwd": (_i32, [
         _vp, _fp, _vp, _fp, _vp,
@@ -134,6 +147,10 @@ def lib() -> ctypes.CDLL:
 
 def strides4(strides) -> ctypes.Array:
     return (ctypes.c_int64 * 4)(*[int(s) for s in strides])
+
+
+def strides3(strides) -> ctypes.Array:
+    return (ctypes.c_int64 * 3)(*[int(s) for s in strides])
 
 
 def check(status: int) -> None:

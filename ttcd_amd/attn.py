@@ -8,7 +8,10 @@ Mirrors the reference's Python interface for this path:
 
 plus ``window_attn`` / ``band_attn`` (the single-window flash-attention call
 those files make, ``flash_attn_func(q, k, v, causal=True,
-window_size=(W-1, 0))``) and ``lse_merge``.
+window_size=(W-1, 0))``), ``lse_merge``, and the packed-sequence forms
+``fused_dual_window_attn_varlen`` / ``band_attn_varlen`` (flash-attention's
+varlen layout, the packed-batch path of fla/layers/attn.py:255-270 that the
+reference's fused prefill declines).
 
 Windows follow flash-attention's ``(W-1, 0)`` convention: key j is visible
 to query i iff 0 <= i - j <= W - 1; a window of None or < 0 means full
@@ -155,6 +158,100 @@ def window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int |
     if w < 1:
         raise ValueError("window must be >= 1")
     return band_attn(q, k, v, 0, w, return_lse=return_lse)
+
+
+def _check_varlen(q, k, v, cu_seqlens, max_seqlen, fn: str):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or t.dim() != 3:
+            raise ValueError(f"{fn}: {name} must be a 3-D packed tensor (total, H, D)")
+    if q.dtype not in _DT:
+        raise ValueError(f"{fn}: dtype {q.dtype} not supported (bfloat16 or float16)")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"{fn}: q, k, v must share one dtype")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError(f"{fn}: q, k, v must be GPU (HIP) tensors")
+    total, H, D = q.shape
+    if k.shape != v.shape or k.shape[0] != total or k.shape[2] != D:
+        raise ValueError(f"{fn}: k/v must be (total, Hkv, D) matching q {tuple(q.shape)}, "
+                         f"got {tuple(k.shape)} / {tuple(v.shape)}")
+    HK = k.shape[1]
+    if H % HK != 0:
+        raise ValueError(f"{fn}: Hq ({H}) must be a multiple of Hkv ({HK})")
+    if (not isinstance(cu_seqlens, torch.Tensor) or cu_seqlens.dim() != 1
+            or cu_seqlens.dtype != torch.int32 or cu_seqlens.numel() < 2):
+        raise ValueError(f"{fn}: cu_seqlens must be a 1-D int32 tensor of nseq + 1 offsets")
+    if not (q.device == k.device == v.device == cu_seqlens.device):
+        raise ValueError(f"{fn}: q, k, v and cu_seqlens must be on one device")
+    if int(max_seqlen) < 1:
+        raise ValueError(f"{fn}: max_seqlen must be >= 1")
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        raise RuntimeError(f"{fn} is forward-only: autograd / gradient inputs are not supported; "
+                           "call it under torch.no_grad() or torch.inference_mode()")
+    return total, H, HK, D, cu_seqlens.numel() - 1
+
+
+def fused_dual_window_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                  cu_seqlens: torch.Tensor, max_seqlen: int,
+                                  window_teacher: int, window_student: int, *,
+                                  return_lse: bool = False):
+    """fused_dual_window_attn on packed sequences (flash-attention's varlen
+    layout): q (total, H, D), k/v (total, HK, D); sequence b is rows
+    cu_seqlens[b] .. cu_seqlens[b+1]-1 (int32 on the GPU, nseq + 1 entries)
+    and attends causally within itself; max_seqlen bounds every length.
+    Windows as fused_dual_window_attn. Returns (o_teacher, o_student) (and
+    (lse_teacher, lse_student), fp32 (H, total), with ``return_lse``). Each
+    sequence's outputs equal fused_dual_window_attn on that sequence alone.
+    cu_seqlens is read on the GPU, so there is no host sync; the kernel
+    clamps every sequence to the packed rows and max_seqlen, and rows
+    outside every sequence are left unwritten."""
+    if window_teacher is not None and window_teacher >= 0:
+        assert window_student <= window_teacher
+    assert window_student >= 1, "window_student must be >= 1"
+    total, H, HK, D, nseq = _check_varlen(q, k, v, cu_seqlens, max_seqlen,
+                                          "fused_dual_window_attn_varlen")
+    wt = -1 if (window_teacher is None or window_teacher < 0) else window_teacher
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    both = torch.empty((2,) + tuple(q.shape), dtype=q.dtype, device=q.device)
+    ot, os_ = both[0], both[1]
+    lse_t = lse_s = None
+    if return_lse:
+        lse_t = torch.empty(H, total, device=q.device, dtype=torch.float32)
+        lse_s = torch.empty(H, total, device=q.device, dtype=torch.float32)
+    L = _lib.lib()
+    _lib.check(L.ttcd_dual_window_attn_varlen_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), ot.data_ptr(), os_.data_ptr(),
+        _lse_ptr(lse_t), _lse_ptr(lse_s), cu_seqlens.data_ptr(), nseq, int(max_seqlen), total,
+        H, HK, D, _lib.strides3(q.stride()), _lib.strides3(k.stride()),
+        _lib.strides3(v.stride()), _lib.strides3(ot.stride()), int(min(wt, 2**31 - 1)),
+        int(min(window_student, 2**31 - 1)), D ** -0.5, _DT[q.dtype], _stream(q.device)))
+    if return_lse:
+        return ot, os_, lse_t, lse_s
+    return ot, os_
+
+
+def band_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     cu_seqlens: torch.Tensor, max_seqlen: int, band_lo: int, band_hi: int, *,
+                     return_lse: bool = False):
+    """band_attn on packed sequences (layout as fused_dual_window_attn_varlen);
+    (0, W) is flash_attn_varlen_func(..., causal=True, window_size=(W-1, 0)).
+    lse: fp32 (H, total)."""
+    total, H, HK, D, nseq = _check_varlen(q, k, v, cu_seqlens, max_seqlen, "band_attn_varlen")
+    if band_hi is None or band_hi < 0:
+        band_hi = max(int(max_seqlen), band_lo + 1)
+    if not (0 <= band_lo < band_hi):
+        raise ValueError(f"band_attn_varlen: need 0 <= band_lo < band_hi, got ({band_lo}, "
+                         f"{band_hi})")
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty(H, total, device=q.device, dtype=torch.float32) if return_lse else None
+    L = _lib.lib()
+    _lib.check(L.ttcd_band_attn_varlen_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), _lse_ptr(lse),
+        cu_seqlens.data_ptr(), nseq, int(max_seqlen), total, H, HK, D,
+        _lib.strides3(q.stride()), _lib.strides3(k.stride()), _lib.strides3(v.stride()),
+        _lib.strides3(o.stride()), int(min(band_lo, 2**31 - 1)), int(min(band_hi, 2**31 - 1)),
+        D ** -0.5, _DT[q.dtype], _stream(q.device)))
+    return (o, lse) if return_lse else o
 
 
 def lse_merge(o_s: torch.Tensor, lse_s: torch.Tensor, o_f: torch.Tensor, lse_f: torch.Tensor,

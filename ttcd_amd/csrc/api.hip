@@ -132,6 +132,8 @@ static ttcd_status set_rows(ttcd::AttnArgs* a, int Tq, int Tk) {
   a->q_off = Tk - Tq;
   a->qb0 = a->q_off / span;
   a->nqb = (Tk + span - 1) / span - a->qb0;
+  a->lse_sh = Tq;
+  a->lse_sb = (int64_t)a->Hq * Tq;
   return TTCD_OK;
 }
 
@@ -210,6 +212,93 @@ ttcd_status ttcd_band_attn_fwd(const void* q, const void* k, const void* v, void
                                float sm_scale, ttcd_dtype dtype, void* stream) {
   return ttcd_band_attn_kv_fwd(q, k, v, o, lse, B, T, T, Hq, Hkv, D, q_stride, k_stride,
                                v_stride, o_stride, band_lo, band_hi, sm_scale, dtype, stream);
+}
+
+// Packed sequences (flash-attention's varlen layout): q / o are (total, Hq, D),
+// k / v (total, Hkv, D), LSEs (Hq, total); sequence b is rows
+// cu_seqlens[b] .. cu_seqlens[b+1]-1. The kernel reads cu_seqlens on the
+// device (no host sync) and clamps every sequence to [0, total) and to
+// max_seqlen rows, so malformed offsets cannot move an access out of the
+// tensors; rows outside every sequence are not written.
+static ttcd_status varlen_args(ttcd::AttnArgs* a, const void* q, const void* k, const void* v,
+                               const void* o, const int32_t* cu_seqlens, int nseq,
+                               int max_seqlen, int total, int Hq, int Hkv, int D,
+                               const int64_t* qs3, const int64_t* ks3, const int64_t* vs3,
+                               const int64_t* os3, float sm_scale, ttcd_dtype dtype) {
+  if (!cu_seqlens) return fail(TTCD_ERR_INVALID_ARGUMENT, "null cu_seqlens");
+  if (!qs3 || !ks3 || !vs3 || !os3) return fail(TTCD_ERR_INVALID_ARGUMENT, "null stride array");
+  if (nseq < 1 || max_seqlen < 1 || total < 0)
+    return fail(TTCD_ERR_INVALID_ARGUMENT,
+                "need nseq >= 1, max_seqlen >= 1, total >= 0 (got %d, %d, %d)", nseq, max_seqlen,
+                total);
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "sm_scale must be finite and > 0");
+  const int64_t qs[4] = {0, qs3[0], qs3[1], qs3[2]}, ks[4] = {0, ks3[0], ks3[1], ks3[2]};
+  const int64_t vs[4] = {0, vs3[0], vs3[1], vs3[2]}, os[4] = {0, os3[0], os3[1], os3[2]};
+  ttcd_status st = check_attn(q, k, v, o, nseq, max_seqlen, Hq, Hkv, D, qs, ks, vs, os, dtype);
+  if (st != TTCD_OK) return st;
+  *a = fill_args(q, k, v, nseq, max_seqlen, Hq, Hkv, qs, ks, vs, os, sm_scale);
+  a->cu_seqlens = cu_seqlens;
+  a->total = total;
+  a->lse_sb = 0;
+  a->lse_sh = total;
+  return TTCD_OK;
+}
+
+ttcd_status ttcd_dual_window_attn_varlen_fwd(const void* q, const void* k, const void* v,
+                                             void* o_t, void* o_s, float* lse_t, float* lse_s,
+                                             const int32_t* cu_seqlens, int nseq, int max_seqlen,
+                                             int total, int Hq, int Hkv, int D,
+                                             const int64_t q_stride[3],
+                                             const int64_t k_stride[3],
+                                             const int64_t v_stride[3],
+                                             const int64_t o_stride[3], int window_t,
+                                             int window_s, float sm_scale, ttcd_dtype dtype,
+                                             void* stream) {
+  ttcd::AttnArgs a;
+  ttcd_status st = varlen_args(&a, q, k, v, o_t, cu_seqlens, nseq, max_seqlen, total, Hq, Hkv,
+                               D, q_stride, k_stride, v_stride, o_stride, sm_scale, dtype);
+  if (st != TTCD_OK) return st;
+  if (!o_s) return fail(TTCD_ERR_INVALID_ARGUMENT, "null student output pointer");
+  if (!aligned16(o_s)) return fail(TTCD_ERR_UNSUPPORTED, "o_s must be 16-byte aligned");
+  if (window_s < 1) return fail(TTCD_ERR_INVALID_ARGUMENT, "window_s must be >= 1 (got %d)", window_s);
+  if (window_t >= 0 && window_s > window_t)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "window_s (%d) must be <= window_t (%d)", window_s,
+                window_t);
+  // full causal: a teacher window no sequence reaches (clamped to each length)
+  if (window_t < 0) window_t = 0x3fffffff;
+  a.o_t = o_t;
+  a.o_s = o_s;
+  a.lse_t = lse_t;
+  a.lse_s = lse_s;
+  a.win_a = window_s;
+  a.win_b = window_t;
+  a.sched = ttcd::make_dual_schedule(max_seqlen, window_s, window_t);
+  return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
+                  "varlen dual-window attention launch");
+}
+
+ttcd_status ttcd_band_attn_varlen_fwd(const void* q, const void* k, const void* v, void* o,
+                                      float* lse, const int32_t* cu_seqlens, int nseq,
+                                      int max_seqlen, int total, int Hq, int Hkv, int D,
+                                      const int64_t q_stride[3], const int64_t k_stride[3],
+                                      const int64_t v_stride[3], const int64_t o_stride[3],
+                                      int band_lo, int band_hi, float sm_scale, ttcd_dtype dtype,
+                                      void* stream) {
+  ttcd::AttnArgs a;
+  ttcd_status st = varlen_args(&a, q, k, v, o, cu_seqlens, nseq, max_seqlen, total, Hq, Hkv, D,
+                               q_stride, k_stride, v_stride, o_stride, sm_scale, dtype);
+  if (st != TTCD_OK) return st;
+  if (band_lo < 0 || band_hi <= band_lo)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi (got %d, %d)", band_lo,
+                band_hi);
+  a.o_t = o;
+  a.lse_t = lse;
+  a.win_a = band_lo;
+  a.win_b = band_hi;
+  a.sched = ttcd::make_band_schedule(max_seqlen, band_lo, band_hi);
+  return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
+                  "varlen band attention launch");
 }
 
 ttcd_status ttcd_lse_merge_fwd(const void* o_s, const float* lse_s, const void* o_f,

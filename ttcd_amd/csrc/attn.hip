@@ -499,8 +499,6 @@ void attn_fwd_kernel(AttnArgs a) {
   const int tid = __builtin_amdgcn_workitem_id_x();
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const Schedule sc = a.sched;
-  const int T_ = a.T;
 
   // Workgroup -> (b, kv head, query block [heaviest first], head in group),
   // XCD-remapped: each XCD sweeps a contiguous run, so the query heads
@@ -514,17 +512,41 @@ void attn_fwd_kernel(AttnArgs a) {
   const int b = rest / a.Hkv;
   const int h = hk * a.G + g;
   const int t0 = qb * kBlockM;
+
+  // Packed sequences: sequence b is rows row0 .. row0 + T_ - 1 of every
+  // tensor, with its own schedule. The bounds are clamped to the packed
+  // tensors and to the launched query blocks, so no cu_seqlens value can
+  // move an access out of them; a workgroup past its sequence's end leaves
+  // before its first barrier.
+  int T_ = a.T;
+  int64_t row0 = 0;
+  Schedule sc = a.sched;
+  if (a.cu_seqlens != nullptr) {
+    const int c0 = __builtin_amdgcn_readfirstlane(a.cu_seqlens[b]);
+    const int c1 = __builtin_amdgcn_readfirstlane(a.cu_seqlens[b + 1]);
+    const int s0 = min(max(c0, 0), a.total);
+    const int s1 = min(max(c1, s0), a.total);
+    T_ = min(s1 - s0, a.nqb * kBlockM);
+    row0 = s0;
+    sc = sc.dual ? make_dual_schedule(T_, a.win_a, a.win_b)
+                 : make_band_schedule(T_, a.win_a, a.win_b);
+    if (t0 >= T_) return;
+  }
   const int r0 = __builtin_amdgcn_readfirstlane(t0 + wave * kWaveRows);
   const int t_last = min(t0 + kBlockM, T_) - 1;
   const int q_off = a.q_off;
-  const int Tq = T_ - q_off;
   // a wave with no row in [q_off, T) computes nothing (it still takes part
   // in the workgroup's loads and barriers)
   const bool wave_valid = (r0 < T_) & (r0 + kWaveRows > q_off);
 
-  const T* qp = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh;
-  const T* kp = uniform_ptr(static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh);
-  const T* vp = uniform_ptr(static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh);
+  const T* qp = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh + row0 * a.q_st;
+  const T* kp =
+      uniform_ptr(static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh + row0 * a.k_st);
+  const T* vp =
+      uniform_ptr(static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh + row0 * a.v_st);
+  // first output row / LSE entry of this (b, h)
+  const int64_t o_base = b * a.o_sb + h * a.o_sh + row0 * a.o_st;
+  const int64_t lse_base = b * a.lse_sb + h * a.lse_sh + row0;
 
   Ctx<D, T> x;
   x.lds = (LDS_AS char*)smem_raw;
@@ -672,8 +694,8 @@ void attn_fwd_kernel(AttnArgs a) {
                               x.lds + (k & 1) * G::STAGE_B + G::TILE_B, settle, side);
     bool stored = false;
     if (DUAL && cur.act == kStudentLast) {
-      T* os = static_cast<T*>(a.o_s) + b * a.o_sb + h * a.o_sh;
-      float* lse_s = a.lse_s ? a.lse_s + ((int64_t)b * a.Hq + h) * Tq : nullptr;
+      T* os = static_cast<T*>(a.o_s) + o_base;
+      float* lse_s = a.lse_s ? a.lse_s + lse_base : nullptr;
       emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, q_off, lane);
       emitted_s = true;
       stored = true;
@@ -693,12 +715,12 @@ void attn_fwd_kernel(AttnArgs a) {
 
   if (wave_valid) {
     if (DUAL && !emitted_s) {
-      T* os = static_cast<T*>(a.o_s) + b * a.o_sb + h * a.o_sh;
-      float* lse_s = a.lse_s ? a.lse_s + ((int64_t)b * a.Hq + h) * Tq : nullptr;
+      T* os = static_cast<T*>(a.o_s) + o_base;
+      float* lse_s = a.lse_s ? a.lse_s + lse_base : nullptr;
       emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, q_off, lane);
     }
-    T* ot = static_cast<T*>(a.o_t) + b * a.o_sb + h * a.o_sh;
-    float* lse_t = a.lse_t ? a.lse_t + ((int64_t)b * a.Hq + h) * Tq : nullptr;
+    T* ot = static_cast<T*>(a.o_t) + o_base;
+    float* lse_t = a.lse_t ? a.lse_t + lse_base : nullptr;
     emit<D, T>(o, m, l, x.c, ot, a.o_st, lse_t, x.qrow, T_, q_off, lane);
   }
 }

@@ -32,6 +32,14 @@ struct AttnArgs {
   int nwg;        // workgroups launched (set by the launcher)
   float c;        // sm_scale * log2(e)
   Schedule sched;
+  int64_t lse_sb, lse_sh;  // LSE strides per batch entry / head (rows are contiguous)
+  // Packed sequences (null for fixed-length batches): sequence b is rows
+  // cu_seqlens[b] .. cu_seqlens[b+1]-1 of every tensor (B sequences, `total`
+  // rows); its schedule is built in the kernel from T = its length and the
+  // windows below (dual: win_a = w_S, win_b = w_T; band: lo, hi).
+  const int* cu_seqlens;
+  int total;
+  int win_a, win_b;
 };
 
 // Launch the dual-window (sched.dual == 1) or single-band kernel.
