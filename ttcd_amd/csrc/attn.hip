@@ -6,21 +6,23 @@
 // calls of the LSE variant (profiling/lse_dual_attn.py:22-29, :143-149).
 //
 // Mapping onto CDNA4
-//   * One workgroup = 8 wavefronts (two groups of 4) sharing each K/V tile:
-//     two query heads of one K/V head over 128 tokens when the GQA group is
-//     even, else one head over 256 tokens. Each wavefront owns 32 query rows.
-//     One workgroup per CU (2 wavefronts per SIMD).
+//   * One workgroup = 4 wavefronts: 128 query tokens of one query head, 32
+//     rows per wavefront. D = 128: two workgroups per CU (64 KiB of LDS
+//     each, <= 256 VGPRs); D = 64: three (32 KiB each, <= 168 VGPRs). The two
+//     or three wavefronts sharing a SIMD come from different workgroups, so
+//     one's barrier and DMA time is filled by another's MFMAs.
 //   * K and V tiles (64 keys) go global -> LDS by DMA
-//     (global_load_lds_dwordx4, no registers), 4 stages deep (each tile is
-//     fetched three slots before its V part is read). Rows are
-//     stored with their 16-byte chunks XOR-swizzled so every operand read
-//     below is free of bank conflicts.
+//     (global_load_lds_dwordx4, no registers) in a two-stage split ring: slot
+//     k reads K(k+1) and V(k), so K(k+2) and V(k+1) are fetched at its start
+//     and have the whole slot to land. Rows are stored with their 16-byte
+//     chunks XOR-swizzled so every operand read below is free of bank
+//     conflicts.
 //   * Scores are produced TRANSPOSED, S^T = K Q^T, with
 //     v_mfma_f32_32x32x16_{bf16,f16}: each lane owns one query (column
 //     lane%32) and 16 of the 32 keys (rows); the other 16 live in lane^32.
 //     Row max / row sum are in-register reductions plus one
 //     v_permlane32_swap, and the online-softmax rescale factor is a
-//     per-lane scalar.
+//     per-lane scalar. Q^T stays in registers for the whole sweep.
 //   * O^T = V^T P^T accumulates in D/32 32x32 fp32 tiles. P^T comes straight
 //     from the score registers (exp2, then rounded to bf16/f16); V^T operands
 //     are read from the row-major V tile with ds_read_b64_tr_b16, which
@@ -29,9 +31,13 @@
 //     16-key step) is matched by the rows each transposed read selects.
 //   * Software pipeline inside each wavefront: while the MFMAs of the next
 //     slot's scores S(k+1) run, the VALU computes exp2 of S(k); the PV MFMAs
-//     of slot k then run while the VALU reduces the row max of S(k+1).
+//     of slot k then run while the VALU sums the row of S(k) and reduces the
+//     row max of S(k+1).
 //   * Workgroups are remapped so each XCD (own L2) sweeps a contiguous run of
-//     (b, kv head, query block, slice); heaviest query blocks first.
+//     (b, kv head, query block, head in group); heaviest query blocks first.
+//   * Packed sequences (cu_seqlens): each workgroup builds its sequence's
+//     schedule from the sequence length, with every bound clamped to the
+//     packed tensors.
 //
 // Numerics follow the reference kernel (fused_dual_attn.py:1-13, :100-107):
 // raw-domain running max, p = exp2(s*c - m*c) with c = sm_scale*log2(e),
