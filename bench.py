@@ -17,7 +17,8 @@ the chunked causal conv at the reference's benchmark shape (GB/s vs 8 TB/s),
 the attention prologue (q/k RMSNorm + rotary) and epilogue (o_proj + dual
 residual RMSNorm) on the same layer, the batch / narrow-gap sweep (fused vs
 LSE variant), the ipttcdv9 prefill end to end (28 layers, T=32768; fused,
-patched and stock paths), numerics at the CPU-runnable config, and the CPU baseline: the fp32 masked
+patched and stock paths; and T=65536, the length of the reference's published
+end-to-end numbers), numerics at the CPU-runnable config, and the CPU baseline: the fp32 masked
 softmax of the reference's CPU path (oracle restatement), query-chunked over
 the band, on a bounded sample of rows, on this host's cores.
 """
@@ -464,6 +465,13 @@ def main() -> int:
             del o_t, o_s
             res["config4_sweep"] = sweep_measure()
             res["e2e_prefill"] = e2e_measure()
+            # the length the reference's end-to-end numbers are quoted at
+            e64 = e2e_measure(steps=3, warmup=1, T=65536, paths=("fused", "stock"))
+            e64["reference_h100_ms"] = {
+                "ipttcdv9_unpatched": 629.0, "ipttcdv9_fused_attn_triton_conv": 526.1,
+                "hardware": "one H100 80GB", "source": "profiling/REPORT.md:25, :321",
+                "note": "other hardware and the reference's generate() prefill; context only"}
+            res["e2e_prefill_64k"] = e64
     if not args.no_numerics:
         res["numerics_config1"] = numerics_report()
         log(f"numerics: {res['numerics_config1']}")
