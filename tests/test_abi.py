@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.lib()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.ttcd_abi_version() == 1
+    assert lib.ttcd_abi_version() == 2
 
 
 def test_status_strings():
@@ -107,7 +107,7 @@ def _varlen_call(fn="dual", **over):
     lib = _lib.lib()
     p = ctypes.c_void_p(0x10000)
     args = dict(cu=p, nseq=2, max_seqlen=64, total=100, Hq=4, Hkv=2, D=64, wt=32, ws=16,
-                lo=0, hi=32, scale=0.125, dtype=_lib.DTYPE_BF16, q=p,
+                lo=0, hi=32, scale=0.125, rescale=8.0, dtype=_lib.DTYPE_BF16, q=p,
                 qs=_lib.strides3([4 * 64, 64, 1]), ks=_lib.strides3([2 * 64, 64, 1]))
     args.update(over)
     common = (args["cu"], args["nseq"], args["max_seqlen"], args["total"], args["Hq"],
@@ -115,10 +115,10 @@ def _varlen_call(fn="dual", **over):
     if fn == "dual":
         return lib.ttcd_dual_window_attn_varlen_fwd(
             args["q"], p, p, p, p, None, None, *common, args["wt"], args["ws"], args["scale"],
-            args["dtype"], None)
+            args["rescale"], args["dtype"], None)
     return lib.ttcd_band_attn_varlen_fwd(
-        args["q"], p, p, p, None, *common, args["lo"], args["hi"], args["scale"], args["dtype"],
-        None)
+        args["q"], p, p, p, None, *common, args["lo"], args["hi"], args["scale"],
+        args["rescale"], args["dtype"], None)
 
 
 @pytest.mark.parametrize("over,status", [
@@ -133,6 +133,9 @@ def _varlen_call(fn="dual", **over):
     (dict(q=ctypes.c_void_p(0x10008)), _lib.TTCD_ERR_UNSUPPORTED),
     (dict(qs=_lib.strides3([4 * 64, 64, 2])), _lib.TTCD_ERR_INVALID_ARGUMENT),
     (dict(scale=float("inf")), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(rescale=-1.0), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(rescale=17.0), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(rescale=float("nan")), _lib.TTCD_ERR_INVALID_ARGUMENT),
 ])
 def test_dual_varlen_rejects(over, status):
     assert _varlen_call("dual", **over) == status
@@ -142,3 +145,19 @@ def test_dual_varlen_rejects(over, status):
 @pytest.mark.parametrize("lo,hi", [(-1, 4), (5, 5), (7, 3)])
 def test_band_varlen_rejects(lo, hi):
     assert _varlen_call("band", lo=lo, hi=hi) == _lib.TTCD_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("rescale", [-0.5, 16.5, float("inf"), float("nan")])
+def test_kv_calls_reject_rescale_threshold(rescale):
+    """rescale_log2 must lie in [0, 16] (0 = the reference kernel's exact running max)."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x10000)
+    qs = _lib.strides4([64 * 4 * 64, 4 * 64, 64, 1])
+    ks = _lib.strides4([64 * 2 * 64, 2 * 64, 64, 1])
+    assert lib.ttcd_dual_window_attn_kv_fwd(
+        p, p, p, p, p, None, None, 1, 64, 64, 4, 2, 64, qs, ks, ks, qs, 32, 16, 0.125, rescale,
+        _lib.DTYPE_BF16, None) == _lib.TTCD_ERR_INVALID_ARGUMENT
+    assert lib.ttcd_band_attn_kv_fwd(
+        p, p, p, p, None, 1, 64, 64, 4, 2, 64, qs, ks, ks, qs, 0, 32, 0.125, rescale,
+        _lib.DTYPE_BF16, None) == _lib.TTCD_ERR_INVALID_ARGUMENT
+    assert b"rescale_log2" in lib.ttcd_last_error()

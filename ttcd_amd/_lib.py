@@ -72,22 +72,22 @@ _SIGS = {
         _vp, _vp, _vp, _vp, _vp, _fp, _fp,
         _i32, _i32, _i32, _i32, _i32, _i32,
         _i64x4, _i64x4, _i64x4, _i64x4,
-        _i32, _i32, ctypes.c_float, _i32, _vp]),
+        _i32, _i32, ctypes.c_float, ctypes.c_float, _i32, _vp]),
     "ttcd_band_attn_kv_fwd": (_i32, [
         _vp, _vp, _vp, _vp, _fp,
         _i32, _i32, _i32, _i32, _i32, _i32,
         _i64x4, _i64x4, _i64x4, _i64x4,
-        _i32, _i32, ctypes.c_float, _i32, _vp]),
+        _i32, _i32, ctypes.c_float, ctypes.c_float, _i32, _vp]),
     "ttcd_dual_window_attn_varlen_fwd": (_i32, [
         _vp, _vp, _vp, _vp, _vp, _fp, _fp, _vp,
         _i32, _i32, _i32, _i32, _i32, _i32,
         _i64x3, _i64x3, _i64x3, _i64x3,
-        _i32, _i32, ctypes.c_float, _i32, _vp]),
+        _i32, _i32, ctypes.c_float, ctypes.c_float, _i32, _vp]),
     "ttcd_band_attn_varlen_fwd": (_i32, [
         _vp, _vp, _vp, _vp, _fp, _vp,
         _i32, _i32, _i32, _i32, _i32, _i32,
         _i64x3, _i64x3, _i64x3, _i64x3,
-        _i32, _i32, ctypes.c_float, _i32, _vp]),
+        _i32, _i32, ctypes.c_float, ctypes.c_float, _i32, _vp]),
     "ttcd_lse_merge_fwd": (_i32, [
         _vp, _fp, _vp, _fp, _vp,
         _i32, _i32, _i32, _i32, _i32, _i64x4, _i32, _vp]),

@@ -27,6 +27,19 @@ from . import _lib
 
 _DT = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
 
+# Lazy online-softmax rescale threshold (log2 units) passed to the kernels:
+# the reference row max moves only when a row's max exceeds it by more than
+# 2^LAZY_RESCALE_LOG2. ``exact_max=True`` passes 0 instead: the exact running
+# max of the reference kernel (profiling/fused_dual_attn.py:100-107), whose
+# bf16 outputs it then reproduces bit for bit except where the dot-product
+# order differs (98.6 % / 99.96 % of teacher / student outputs at config 1),
+# for ~5 % more time.
+LAZY_RESCALE_LOG2 = 8.0
+
+
+def _rescale(exact_max: bool) -> float:
+    return 0.0 if exact_max else LAZY_RESCALE_LOG2
+
 
 def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
@@ -74,7 +87,7 @@ def _lse_ptr(t):
 
 def fused_dual_window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                            window_teacher: int, window_student: int, block_n: int = 64,
-                           *, return_lse: bool = False):
+                           *, return_lse: bool = False, exact_max: bool = False):
     """Returns (o_teacher, o_student) of one pass over K/V.
 
     Same call as profiling/fused_dual_attn.py:244: q (B, T, H, D), k/v
@@ -84,7 +97,8 @@ def fused_dual_window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     always sweeps 64-key tiles. Unlike the reference, window_student may be
     any value >= 1 and teacher == student windows of any alignment are exact.
     With ``return_lse=True`` also returns (lse_teacher, lse_student), fp32
-    natural-log (B, H, T).
+    natural-log (B, H, T). ``exact_max=True`` keeps the reference kernel's
+    exact running max (see LAZY_RESCALE_LOG2).
 
     k / v may be longer than q (Tk > Tq, a prefill onto a populated cache):
     the queries are then the last Tq positions, flash-attention's
@@ -114,14 +128,15 @@ def fused_dual_window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         _lse_ptr(lse_t), _lse_ptr(lse_s), B, T, k.shape[1], H, HK, D,
         _lib.strides4(q.stride()), _lib.strides4(k.stride()), _lib.strides4(v.stride()),
         _lib.strides4(ot.stride()), int(min(window_teacher, 2**31 - 1)),
-        int(min(window_student, 2**31 - 1)), D ** -0.5, _DT[q.dtype], _stream(q.device)))
+        int(min(window_student, 2**31 - 1)), D ** -0.5, _rescale(exact_max), _DT[q.dtype],
+        _stream(q.device)))
     if return_lse:
         return ot, os_, lse_t, lse_s
     return ot, os_
 
 
 def band_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, band_lo: int, band_hi: int,
-              *, return_lse: bool = False):
+              *, return_lse: bool = False, exact_max: bool = False):
     """Causal attention over keys j with band_lo <= i - j < band_hi.
 
     (0, W) is flash_attn_func(q, k, v, causal=True, window_size=(W-1, 0));
@@ -143,12 +158,12 @@ def band_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, band_lo: int, b
         B, T, Tk, H, HK, D,
         _lib.strides4(q.stride()), _lib.strides4(k.stride()), _lib.strides4(v.stride()),
         _lib.strides4(o.stride()), int(min(band_lo, 2**31 - 1)), int(min(band_hi, 2**31 - 1)),
-        D ** -0.5, _DT[q.dtype], _stream(q.device)))
+        D ** -0.5, _rescale(exact_max), _DT[q.dtype], _stream(q.device)))
     return (o, lse) if return_lse else o
 
 
 def window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int | None,
-                *, return_lse: bool = False):
+                *, return_lse: bool = False, exact_max: bool = False):
     """flash_attn_func(q, k, v, causal=True, window_size=(window-1, 0)) on gfx950;
     window None or < 0 = full causal. The "two separate calls" comparator.
     With k / v longer than q (a cached prefill), the queries are the last Tq
@@ -157,7 +172,7 @@ def window_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int |
     w = T if (window is None or window < 0) else window
     if w < 1:
         raise ValueError("window must be >= 1")
-    return band_attn(q, k, v, 0, w, return_lse=return_lse)
+    return band_attn(q, k, v, 0, w, return_lse=return_lse, exact_max=exact_max)
 
 
 def _check_varlen(q, k, v, cu_seqlens, max_seqlen, fn: str):
@@ -193,7 +208,7 @@ def _check_varlen(q, k, v, cu_seqlens, max_seqlen, fn: str):
 def fused_dual_window_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                   cu_seqlens: torch.Tensor, max_seqlen: int,
                                   window_teacher: int, window_student: int, *,
-                                  return_lse: bool = False):
+                                  return_lse: bool = False, exact_max: bool = False):
     """fused_dual_window_attn on packed sequences (flash-attention's varlen
     layout): q (total, H, D), k/v (total, HK, D); sequence b is rows
     cu_seqlens[b] .. cu_seqlens[b+1]-1 (int32 on the GPU, nseq + 1 entries)
@@ -223,7 +238,8 @@ def fused_dual_window_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
         _lse_ptr(lse_t), _lse_ptr(lse_s), cu_seqlens.data_ptr(), nseq, int(max_seqlen), total,
         H, HK, D, _lib.strides3(q.stride()), _lib.strides3(k.stride()),
         _lib.strides3(v.stride()), _lib.strides3(ot.stride()), int(min(wt, 2**31 - 1)),
-        int(min(window_student, 2**31 - 1)), D ** -0.5, _DT[q.dtype], _stream(q.device)))
+        int(min(window_student, 2**31 - 1)), D ** -0.5, _rescale(exact_max), _DT[q.dtype],
+        _stream(q.device)))
     if return_lse:
         return ot, os_, lse_t, lse_s
     return ot, os_
@@ -231,7 +247,7 @@ def fused_dual_window_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
 
 def band_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      cu_seqlens: torch.Tensor, max_seqlen: int, band_lo: int, band_hi: int, *,
-                     return_lse: bool = False):
+                     return_lse: bool = False, exact_max: bool = False):
     """band_attn on packed sequences (layout as fused_dual_window_attn_varlen);
     (0, W) is flash_attn_varlen_func(..., causal=True, window_size=(W-1, 0)).
     lse: fp32 (H, total)."""
@@ -250,7 +266,7 @@ def band_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         cu_seqlens.data_ptr(), nseq, int(max_seqlen), total, H, HK, D,
         _lib.strides3(q.stride()), _lib.strides3(k.stride()), _lib.strides3(v.stride()),
         _lib.strides3(o.stride()), int(min(band_lo, 2**31 - 1)), int(min(band_hi, 2**31 - 1)),
-        D ** -0.5, _DT[q.dtype], _stream(q.device)))
+        D ** -0.5, _rescale(exact_max), _DT[q.dtype], _stream(q.device)))
     return (o, lse) if return_lse else o
 
 
@@ -278,7 +294,8 @@ def lse_merge(o_s: torch.Tensor, lse_s: torch.Tensor, o_f: torch.Tensor, lse_f: 
     return o_t
 
 
-def lse_dual_window_attn(q, k, v, window_teacher: int, window_student: int):
+def lse_dual_window_attn(q, k, v, window_teacher: int, window_student: int, *,
+                         exact_max: bool = False):
     """Student = window WS (with LSE); far band [WS, WT) (with LSE); teacher =
     exact LSE merge. profiling/lse_dual_attn.py:16-39 (flash-attn there, the
     gfx950 band kernel here). Requires WS < WT (AssertionError otherwise)."""
@@ -287,10 +304,10 @@ def lse_dual_window_attn(q, k, v, window_teacher: int, window_student: int):
     WT = Tk if (window_teacher is None or window_teacher < 0) else window_teacher
     WS = window_student
     assert WS < WT
-    o_s, lse_s = window_attn(q, k, v, WS, return_lse=True)
+    o_s, lse_s = window_attn(q, k, v, WS, return_lse=True, exact_max=exact_max)
     if Tk <= WS:
         return o_s, o_s
-    o_f, lse_f = band_attn(q, k, v, WS, WT, return_lse=True)
+    o_f, lse_f = band_attn(q, k, v, WS, WT, return_lse=True, exact_max=exact_max)
     # rows at absolute positions below WS have an empty far band
     o_t = lse_merge(o_s, lse_s, o_f, lse_f, row_start=max(0, WS - (Tk - Tq)))
     return o_t, o_s

@@ -67,6 +67,15 @@ ttcd_status check_attn(const void* q, const void* k, const void* v, const void* 
   return TTCD_OK;
 }
 
+// The lazy-rescale threshold: finite, 0 (exact running max) .. 16 (keeps every
+// probability below 2^16 times its row's largest, far from fp32 overflow).
+ttcd_status check_rescale(float rescale_log2) {
+  if (!(rescale_log2 >= 0.f && rescale_log2 <= 16.f))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "rescale_log2 must be in [0, 16] (got %g)",
+                (double)rescale_log2);
+  return TTCD_OK;
+}
+
 ttcd::AttnArgs fill_args(const void* q, const void* k, const void* v, int B, int T, int Hq,
                          int Hkv, const int64_t* qs, const int64_t* ks, const int64_t* vs,
                          const int64_t* os, float sm_scale) {
@@ -143,9 +152,10 @@ ttcd_status ttcd_dual_window_attn_kv_fwd(const void* q, const void* k, const voi
                                          const int64_t q_stride[4], const int64_t k_stride[4],
                                          const int64_t v_stride[4], const int64_t o_stride[4],
                                          int window_t, int window_s, float sm_scale,
-                                         ttcd_dtype dtype, void* stream) {
+                                         float rescale_log2, ttcd_dtype dtype, void* stream) {
   ttcd_status st =
       check_attn(q, k, v, o_t, B, Tk, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
+  if (st == TTCD_OK) st = check_rescale(rescale_log2);
   if (st != TTCD_OK) return st;
   if (!o_s) return fail(TTCD_ERR_INVALID_ARGUMENT, "null student output pointer");
   if (!aligned16(o_s)) return fail(TTCD_ERR_UNSUPPORTED, "o_s must be 16-byte aligned");
@@ -164,6 +174,7 @@ ttcd_status ttcd_dual_window_attn_kv_fwd(const void* q, const void* k, const voi
   a.o_s = o_s;
   a.lse_t = lse_t;
   a.lse_s = lse_s;
+  a.rescale_log2 = rescale_log2;
   a.sched = ttcd::make_dual_schedule(Tk, window_s, window_t);
   return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
                   "dual-window attention launch");
@@ -177,17 +188,18 @@ ttcd_status ttcd_dual_window_attn_fwd(const void* q, const void* k, const void* 
                                       float sm_scale, ttcd_dtype dtype, void* stream) {
   return ttcd_dual_window_attn_kv_fwd(q, k, v, o_t, o_s, lse_t, lse_s, B, T, T, Hq, Hkv, D,
                                       q_stride, k_stride, v_stride, o_stride, window_t, window_s,
-                                      sm_scale, dtype, stream);
+                                      sm_scale, ttcd::kDefaultRescaleLog2, dtype, stream);
 }
 
 ttcd_status ttcd_band_attn_kv_fwd(const void* q, const void* k, const void* v, void* o,
                                   float* lse, int B, int Tq, int Tk, int Hq, int Hkv, int D,
                                   const int64_t q_stride[4], const int64_t k_stride[4],
                                   const int64_t v_stride[4], const int64_t o_stride[4],
-                                  int band_lo, int band_hi, float sm_scale, ttcd_dtype dtype,
-                                  void* stream) {
+                                  int band_lo, int band_hi, float sm_scale, float rescale_log2,
+                                  ttcd_dtype dtype, void* stream) {
   ttcd_status st =
       check_attn(q, k, v, o, B, Tk, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
+  if (st == TTCD_OK) st = check_rescale(rescale_log2);
   if (st != TTCD_OK) return st;
   if (band_lo < 0 || band_hi <= band_lo)
     return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi (got %d, %d)", band_lo,
@@ -200,6 +212,7 @@ ttcd_status ttcd_band_attn_kv_fwd(const void* q, const void* k, const void* v, v
   if (st != TTCD_OK) return st;
   a.o_t = o;
   a.lse_t = lse;
+  a.rescale_log2 = rescale_log2;
   a.sched = ttcd::make_band_schedule(Tk, band_lo, band_hi);
   return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
                   "band attention launch");
@@ -211,7 +224,8 @@ ttcd_status ttcd_band_attn_fwd(const void* q, const void* k, const void* v, void
                                const int64_t o_stride[4], int band_lo, int band_hi,
                                float sm_scale, ttcd_dtype dtype, void* stream) {
   return ttcd_band_attn_kv_fwd(q, k, v, o, lse, B, T, T, Hq, Hkv, D, q_stride, k_stride,
-                               v_stride, o_stride, band_lo, band_hi, sm_scale, dtype, stream);
+                               v_stride, o_stride, band_lo, band_hi, sm_scale,
+                               ttcd::kDefaultRescaleLog2, dtype, stream);
 }
 
 // Packed sequences (flash-attention's varlen layout): q / o are (total, Hq, D),
@@ -224,8 +238,10 @@ static ttcd_status varlen_args(ttcd::AttnArgs* a, const void* q, const void* k, 
                                const void* o, const int32_t* cu_seqlens, int nseq,
                                int max_seqlen, int total, int Hq, int Hkv, int D,
                                const int64_t* qs3, const int64_t* ks3, const int64_t* vs3,
-                               const int64_t* os3, float sm_scale, ttcd_dtype dtype) {
+                               const int64_t* os3, float sm_scale, float rescale_log2,
+                               ttcd_dtype dtype) {
   if (!cu_seqlens) return fail(TTCD_ERR_INVALID_ARGUMENT, "null cu_seqlens");
+  if (check_rescale(rescale_log2) != TTCD_OK) return TTCD_ERR_INVALID_ARGUMENT;
   if (!qs3 || !ks3 || !vs3 || !os3) return fail(TTCD_ERR_INVALID_ARGUMENT, "null stride array");
   if (nseq < 1 || max_seqlen < 1 || total < 0)
     return fail(TTCD_ERR_INVALID_ARGUMENT,
@@ -242,6 +258,7 @@ static ttcd_status varlen_args(ttcd::AttnArgs* a, const void* q, const void* k, 
   a->total = total;
   a->lse_sb = 0;
   a->lse_sh = total;
+  a->rescale_log2 = rescale_log2;
   return TTCD_OK;
 }
 
@@ -253,11 +270,12 @@ ttcd_status ttcd_dual_window_attn_varlen_fwd(const void* q, const void* k, const
                                              const int64_t k_stride[3],
                                              const int64_t v_stride[3],
                                              const int64_t o_stride[3], int window_t,
-                                             int window_s, float sm_scale, ttcd_dtype dtype,
-                                             void* stream) {
+                                             int window_s, float sm_scale, float rescale_log2,
+                                             ttcd_dtype dtype, void* stream) {
   ttcd::AttnArgs a;
   ttcd_status st = varlen_args(&a, q, k, v, o_t, cu_seqlens, nseq, max_seqlen, total, Hq, Hkv,
-                               D, q_stride, k_stride, v_stride, o_stride, sm_scale, dtype);
+                               D, q_stride, k_stride, v_stride, o_stride, sm_scale, rescale_log2,
+                               dtype);
   if (st != TTCD_OK) return st;
   if (!o_s) return fail(TTCD_ERR_INVALID_ARGUMENT, "null student output pointer");
   if (!aligned16(o_s)) return fail(TTCD_ERR_UNSUPPORTED, "o_s must be 16-byte aligned");
@@ -283,11 +301,12 @@ ttcd_status ttcd_band_attn_varlen_fwd(const void* q, const void* k, const void* 
                                       int max_seqlen, int total, int Hq, int Hkv, int D,
                                       const int64_t q_stride[3], const int64_t k_stride[3],
                                       const int64_t v_stride[3], const int64_t o_stride[3],
-                                      int band_lo, int band_hi, float sm_scale, ttcd_dtype dtype,
-                                      void* stream) {
+                                      int band_lo, int band_hi, float sm_scale,
+                                      float rescale_log2, ttcd_dtype dtype, void* stream) {
   ttcd::AttnArgs a;
   ttcd_status st = varlen_args(&a, q, k, v, o, cu_seqlens, nseq, max_seqlen, total, Hq, Hkv, D,
-                               q_stride, k_stride, v_stride, o_stride, sm_scale, dtype);
+                               q_stride, k_stride, v_stride, o_stride, sm_scale, rescale_log2,
+                               dtype);
   if (st != TTCD_OK) return st;
   if (band_lo < 0 || band_hi <= band_lo)
     return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi (got %d, %d)", band_lo,

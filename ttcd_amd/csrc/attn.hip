@@ -44,7 +44,8 @@
 // the m == -inf -> 0 guard, P rounded to the input dtype before PV, l summed
 // from the unrounded fp32 p, epilogue acc * (1/l) rounded to nearest-even.
 // The running max used in exp2 moves only when a row's max grows by more than
-// 2^8 (lazy rescale; softmax is invariant to it up to rounding).
+// 2^rescale_log2 (lazy rescale, default 2^8; softmax is invariant to it up to
+// rounding); rescale_log2 = 0 keeps the exact running max of the reference.
 //
 // Built with -fno-honor-nans -mno-amdgpu-ieee (ttcd_amd/build.py): no value
 // here is NaN for finite inputs (masked scores are -inf, every test below is
@@ -252,9 +253,6 @@ __device__ __forceinline__ void dma_tile(uint32_t dst, const T* base, int64_t st
     dma16(tile, voff, dst + (wave + kWaves * i) * 1024);
   }
 }
-
-// Rescale threshold of the lazy online softmax (log2 units).
-constexpr float kRescaleLog2 = 8.0f;
 
 // Key index of S^T accumulator element e of key block kt for this lane.
 __device__ __forceinline__ int key_of(int j0, int kt, int e, int half) {
@@ -585,6 +583,7 @@ void attn_fwd_kernel(AttnArgs a) {
 
   const WaveSlots wsl(sc, r0);
   const int64_t kst = a.k_st, vst = a.v_st;
+  const float rescale_log2 = a.rescale_log2;
   // DMA of the K (or V) tile of tile index n into the K (V) half of stage s.
   auto dma_half = [&](bool is_k, int n, int s) __attribute__((always_inline)) {
     const int j0 = sc.tile_start(n);
@@ -666,7 +665,8 @@ void attn_fwd_kernel(AttnArgs a) {
     SlotInfo nxt;
     // Mask S(k) if needed, then the reference max of slot k (lazy rescale):
     // moved, and O^T / l rescaled, only when some row's max exceeds it by
-    // more than 2^kRescaleLog2. Returns m*c for the exp2 of slot k.
+    // more than 2^rescale_log2 (0: whenever it grows, the reference kernel's
+    // exact running max). Returns m*c for the exp2 of slot k.
     auto settle = [&]() __attribute__((always_inline)) {
       float mx = mx_lane;
       if (__builtin_expect(cur.mask, 0)) {
@@ -682,7 +682,7 @@ void attn_fwd_kernel(AttnArgs a) {
       mx = xhalf_max(mx);
       const bool active = cur.act != kSkip;
       const float m_new = active ? fmaxf(m, mx) : m;
-      const bool grow = (m_new > m) & ((m == -INFINITY) | ((m_new - m) * x.c > kRescaleLog2));
+      const bool grow = (m_new > m) & ((m == -INFINITY) | ((m_new - m) * x.c > rescale_log2));
       if (__builtin_expect(__any(grow) != 0, 0)) {
         const float mc_new = (m_new == -INFINITY) ? 0.f : m_new * x.c;
         const float alpha = fast_exp2(fmaf(m, x.c, -mc_new));

@@ -31,6 +31,8 @@ struct AttnArgs {
   int nqb;        // query tiles of kBlockM tokens per (b, h) launched
   int nwg;        // workgroups launched (set by the launcher)
   float c;        // sm_scale * log2(e)
+  float rescale_log2;  // lazy online softmax: the reference max moves when a row max
+                       // exceeds it by more than 2^rescale_log2 (0: exact running max)
   Schedule sched;
   int64_t lse_sb, lse_sh;  // LSE strides per batch entry / head (rows are contiguous)
   // Packed sequences (null for fixed-length batches): sequence b is rows
@@ -41,6 +43,10 @@ struct AttnArgs {
   int total;
   int win_a, win_b;
 };
+
+// Default lazy-rescale threshold (log2 units) of the attention entry points
+// that take none.
+constexpr float kDefaultRescaleLog2 = 8.0f;
 
 // Launch the dual-window (sched.dual == 1) or single-band kernel.
 hipError_t launch_attn(const AttnArgs& a, int D, Elem dtype, hipStream_t stream);
