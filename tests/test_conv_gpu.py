@@ -63,3 +63,28 @@ def test_module_api_and_identity_init(gpu):
     conv = conv.cuda().to(torch.bfloat16)
     x = torch.randn(2, 3, 64, D).to(torch.bfloat16).cuda()
     assert torch.equal(causal_dwconv_chunked(x, conv), x)
+
+
+def _random_conv_case(i):
+    import random
+    r = random.Random(500 + i)
+    b, nch = r.randint(1, 3), r.randint(1, 4)
+    C = r.choice([1, 2, r.randint(1, 40), r.randint(16, 300)])
+    D = r.choice([8, 16, 24, 64, 136, 3072, r.randint(1, 200)])
+    K = r.choice([1, 2, 3, 4, 5, 5, 6, 7, 8, r.randint(9, 64)])
+    xdt = r.choice([torch.bfloat16, torch.bfloat16, torch.float16, torch.float32])
+    wdt = r.choice([xdt, torch.float32, torch.bfloat16])
+    return (b, nch, C, D), K, xdt, wdt
+
+
+@pytest.mark.parametrize("i", range(60))
+@torch.inference_mode()
+def test_random_shapes_bitwise_vs_oracle(gpu, i):
+    """Seeded random shapes (vector and scalar kernels, K up to 64, every dtype pair)
+    bitwise against the fixed-order oracle."""
+    shape, K, xdt, wdt = _random_conv_case(i)
+    print(f"case {i}: shape {shape} K {K} x {xdt} w {wdt}", flush=True)
+    g = torch.Generator().manual_seed(900 + i)
+    x = torch.randn(*shape, generator=g).to(xdt)
+    w = torch.randn(shape[-1], K, generator=g).to(wdt)
+    assert _bits_equal(_run(x, w), conv_ref.dwconv_c(x, w)), f"case {i}"

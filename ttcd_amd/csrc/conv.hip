@@ -33,7 +33,14 @@ struct Cvt<__bf16> {
 template <>
 struct Cvt<_Float16> {
   __device__ static float to_f(_Float16 v) { return static_cast<float>(v); }
-  __device__ static _Float16 from_f(float v) { return static_cast<_Float16>(v); }
+  // The empty asm pins the fp32 sum in a register first. Without it the compiler
+  // fuses the last tap's fma with this conversion (v_fma_mix{lo,hi}_f16), which
+  // rounds once from the exact value instead of fp32-then-fp16 as the reference
+  // conv does, and about one output in 8K differs in its last bit.
+  __device__ static _Float16 from_f(float v) {
+    __asm__("" : "+v"(v));
+    return static_cast<_Float16>(v);
+  }
 };
 template <>
 struct Cvt<float> {
