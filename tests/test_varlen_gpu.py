@@ -122,3 +122,45 @@ def test_varlen_argument_checks(gpu):
         fused_dual_window_attn_varlen(q, k, v, cu, 0, 16, 8)
     with pytest.raises(AssertionError):
         fused_dual_window_attn_varlen(q, k, v, cu, 20, 8, 16)
+
+
+def _random_varlen_case(i):
+    import random
+    r = random.Random(3000 + i)
+    lens = [r.choice([0, 1, r.randint(1, 130), r.randint(100, 1200)]) for _ in range(r.randint(1, 6))]
+    D = r.choice([64, 128])
+    kv_heads = r.choice([1, 2, 4])
+    heads = kv_heads * r.choice([1, 2, 3])
+    mx = max(max(lens), 1)
+    wt = r.choice([-1, r.randint(1, mx + 200), r.randint(1, 300)])
+    ws = r.choice([1, r.randint(1, 300), wt if wt > 0 else mx])
+    dtype = r.choice([torch.bfloat16, torch.float16])
+    return lens, heads, kv_heads, D, wt, ws, dtype, r.random() < 0.3
+
+
+@pytest.mark.parametrize("i", range(40))
+@torch.inference_mode()
+def test_random_varlen_equals_per_sequence_calls(gpu, i):
+    """Seeded random packings, head shapes, windows and dtypes: every sequence
+    bit-identical to the fixed-length call on it alone, in the chosen rescale mode."""
+    from ttcd_amd import fused_dual_window_attn, fused_dual_window_attn_varlen
+    lens, heads, kv_heads, D, wt, ws, dtype, exact = _random_varlen_case(i)
+    print(f"case {i}: lens {lens} H {heads}/{kv_heads} D {D} wt {wt} ws {ws} {dtype} "
+          f"exact_max {exact}", flush=True)
+    q, k, v, cu = _packed(lens, heads, kv_heads, D, seed=400 + i, dtype=dtype)
+    if wt > 0:
+        ws = min(ws, wt)
+    ot, os_, lt, ls = fused_dual_window_attn_varlen(q, k, v, cu, max(max(lens), 1), wt, ws,
+                                                    return_lse=True, exact_max=exact)
+    torch.cuda.synchronize()
+    for s0, s1 in _offsets(lens):
+        if s1 == s0:
+            continue
+        qs, ks, vs = (t[s0:s1].unsqueeze(0) for t in (q, k, v))
+        wt_ref = (s1 - s0) if wt < 0 else wt
+        rt, rs, rlt, rls = fused_dual_window_attn(qs, ks, vs, wt_ref, min(ws, wt_ref),
+                                                  return_lse=True, exact_max=exact)
+        assert torch.equal(ot[s0:s1], rt[0]), (i, s0, s1)
+        assert torch.equal(os_[s0:s1], rs[0]), (i, s0, s1)
+        assert torch.equal(lt[:, s0:s1], rlt[0]), (i, s0, s1)
+        assert torch.equal(ls[:, s0:s1], rls[0]), (i, s0, s1)

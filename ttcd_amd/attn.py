@@ -232,6 +232,8 @@ def fused_dual_window_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     if return_lse:
         lse_t = torch.empty(H, total, device=q.device, dtype=torch.float32)
         lse_s = torch.empty(H, total, device=q.device, dtype=torch.float32)
+    if total == 0:  # every sequence empty: nothing to launch
+        return (ot, os_, lse_t, lse_s) if return_lse else (ot, os_)
     L = _lib.lib()
     _lib.check(L.ttcd_dual_window_attn_varlen_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), ot.data_ptr(), os_.data_ptr(),
@@ -260,6 +262,8 @@ def band_attn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     q, k, v = _ready(q), _ready(k), _ready(v)
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(H, total, device=q.device, dtype=torch.float32) if return_lse else None
+    if total == 0:  # every sequence empty: nothing to launch
+        return (o, lse) if return_lse else o
     L = _lib.lib()
     _lib.check(L.ttcd_band_attn_varlen_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), _lse_ptr(lse),
