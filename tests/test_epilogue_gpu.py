@@ -141,3 +141,16 @@ def test_headline_shape():
     rows = torch.arange(0, T, 37)
     _check(a_t[:, rows].cpu(), a_s[:, rows].cpu(), r[:, rows].cpu(), w.cpu(), 1e-6,
            y_t[:, rows], res_out[:, rows], y_s[:, rows])
+
+
+@pytest.mark.parametrize("i", range(30))
+def test_random_shapes_match_oracle(i):
+    """Seeded random batches, lengths, hidden sizes (multiples of 8 up to 2048) and
+    dtype pairs against the oracle, with the bounds of test_matches_oracle."""
+    import random
+    r = random.Random(6000 + i)
+    B, T, H = r.choice([1, 2, 3]), r.randint(1, 600), 8 * r.randint(1, 256)
+    dtype = r.choice([torch.bfloat16, torch.bfloat16, torch.float16])
+    wdt = r.choice([dtype, dtype, torch.float32])
+    print(f"case {i}: B {B} T {T} H {H} {dtype} w {wdt}", flush=True)
+    test_matches_oracle(B, T, H, dtype, wdt)

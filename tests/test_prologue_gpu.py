@@ -169,3 +169,25 @@ def test_headline_shape_sampled_rows():
         assert rep["max_ulp"] <= 1 and rep["bit_equal_pct"] > 99.0, rep
         assert torch.equal(got[:, rows].cpu(), prologue_ref.rope_ref(
             n[:, rows].cpu(), cos[rows].cpu(), sin[rows].cpu()))
+
+
+def _random_prologue_case(i):
+    import random
+    r = random.Random(5000 + i)
+    Hkv = r.choice([1, 2, 4, 8])
+    return dict(B=r.choice([1, 2]), T=r.randint(1, 700), Hq=Hkv * r.choice([1, 2, 3]), Hkv=Hkv,
+                D=r.choice([64, 128]), norm=r.random() < 0.75,
+                dtype=r.choice([torch.bfloat16, torch.bfloat16, torch.float16]),
+                wdt=r.choice(["x", "x", torch.float32]), offset=r.choice([0, 0, r.randint(1, 70000)]),
+                base=r.choice([1e4, 1e5, 1e6]))
+
+
+@pytest.mark.parametrize("i", range(30))
+def test_random_shapes_match_oracle(i):
+    """Seeded random batches, lengths, head counts, head dims, dtypes, weight dtypes,
+    positions and rotary bases against the oracle, with the bounds of test_matches_oracle."""
+    c = _random_prologue_case(i)
+    print(f"case {i}: {c}", flush=True)
+    wdt = c["dtype"] if c["wdt"] == "x" else c["wdt"]
+    test_matches_oracle(c["B"], c["T"], c["Hq"], c["Hkv"], c["D"], c["norm"], c["dtype"], wdt,
+                        c["offset"], c["base"])
