@@ -41,7 +41,8 @@ def test_band_pair_counts_brute_force():
 
 
 def test_headline_flop_constants():
-    # SURVEY / BASELINE figures: P(65536, 8192) and the teacher/student band FLOPs.
+    # Headline figures: P(65536, 8192) = 8192*8193/2 + (65536-8192)*8192 pairs per head,
+    # and the teacher / student band FLOPs (4*D per pair, B=1, Hq=16, D=128).
     assert attn_ref.window_pairs(65536, 8192) == 503_320_576
     assert attn_ref.window_pairs(2048, 512) == 917_760
     assert abs(attn_ref.attn_flops(1, 16, 128, 65536, 8192) - 4.1232e12) < 1e8
