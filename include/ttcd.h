@@ -55,7 +55,10 @@ int ttcd_abi_version(void);
  *
  * q: (B, T, Hq, D); k, v: (B, T, Hkv, D); o_t, o_s: (B, T, Hq, D), all of
  * `dtype` (BF16 or F16), D in {64, 128}, Hq % Hkv == 0, head h reads kv head
- * h / (Hq / Hkv). *_stride[4] = element strides of (b, t, h, d); d-stride 1.
+ * h / (Hq / Hkv). *_stride[4] = element strides of (b, t, h, d); d-stride 1,
+ * the others non-negative multiples of 8; the k and v token strides at most
+ * 2^25 (TTCD_ERR_UNSUPPORTED above). These stride rules hold for every
+ * attention entry point below.
  * o_t and o_s share o_stride. window_t >= T (or < 0) means full causal.
  * Requires 1 <= window_s <= window_t. lse_t / lse_s may be NULL; when given
  * they receive log(sum_j exp(sm_scale * q.k_j)) over each window, (B, Hq, T).

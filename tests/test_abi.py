@@ -71,6 +71,7 @@ def _attn_call(fn="dual", **over):
     (dict(qs=_lib.strides4([64 * 4 * 64, 4 * 64, 64, 2])), _lib.TTCD_ERR_INVALID_ARGUMENT),
     (dict(qs=_lib.strides4([64 * 4 * 64, 4 * 64 + 4, 64, 1])), _lib.TTCD_ERR_UNSUPPORTED),
     (dict(scale=0.0), _lib.TTCD_ERR_INVALID_ARGUMENT),
+    (dict(ks=_lib.strides4([0, 2**25 + 8, 64, 1])), _lib.TTCD_ERR_UNSUPPORTED),  # 32-bit tile offsets
 ])
 def test_dual_rejects(over, status):
     assert _attn_call("dual", **over) == status

@@ -36,6 +36,9 @@ ttcd_status from_hip(hipError_t e, const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Largest K/V token stride (elements) the tile loads' 32-bit lane offsets reach.
+constexpr int64_t kMaxTokenStride = int64_t(1) << 25;
+
 // Checks shared by both attention entry points.
 ttcd_status check_attn(const void* q, const void* k, const void* v, const void* o, int B, int T,
                        int Hq, int Hkv, int D, const int64_t* qs, const int64_t* ks,
@@ -61,6 +64,11 @@ ttcd_status check_attn(const void* q, const void* k, const void* v, const void* 
                     "strides must be non-negative multiples of 8 elements (16-byte rows)");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return fail(TTCD_ERR_UNSUPPORTED, "tensor base pointers must be 16-byte aligned");
+  // The K/V tile loads address a lane's chunk with a 32-bit byte offset from the
+  // tile's first key: 63 token strides of 2-byte elements plus one row must fit.
+  if (ks[1] > kMaxTokenStride || vs[1] > kMaxTokenStride)
+    return fail(TTCD_ERR_UNSUPPORTED, "k/v token stride above %lld elements",
+                (long long)kMaxTokenStride);
   const int64_t nqb = (T + ttcd::kBlockM - 1) / ttcd::kBlockM;
   if ((int64_t)B * Hq * nqb > 0x7fffffffLL)  // bound on workgroups for either geometry
     return fail(TTCD_ERR_UNSUPPORTED, "grid too large");
