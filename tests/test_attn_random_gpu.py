@@ -5,24 +5,63 @@ third of the cases) a cached prefill (Tq < Tk) from a fixed seed, so every run
 checks the same cases. Windows cover w_S = 1, w_S = w_T, w_T >= T, full-causal
 teachers, and unaligned values. Checks:
   * both outputs and both LSEs of fused_dual_window_attn against the fp32
-    oracle (the tolerances of tests/test_attn_gpu.py; LSE within 1e-3);
+    oracle (the tolerances of tests/test_attn_gpu.py, with the mean bounds
+    scaled to the output's magnitude, see _assert_close; LSE within 1e-3);
   * the LSE-combination variant's teacher against the same oracle (w_S < w_T),
     allowing for its second rounding;
   * fused_dual_window_attn with exact_max=True against the oracle.
 """
 from __future__ import annotations
 
+import os
 import random
 
 import pytest
 import torch
 
 from oracle import attn_ref
-from test_attn_gpu import _assert_close
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 120
+# TTCD_RANDOM_CASES widens the sweep for a one-off deeper check (same seeds, more cases).
+N_CASES = int(os.environ.get("TTCD_RANDOM_CASES", "400"))
+
+
+def _unit_roundoff(dtype):
+    return 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+
+
+def _assert_close(actual, expected, dtype, what, merged=False):
+    """The reference test's bounds (tests/test_attn_gpu.py, from
+    test_fused_dual_attn.py:88-110) plus the north-star bounds, with both mean
+    bounds scaled to the output's magnitude. The absolute means (4e-4 bf16 /
+    6e-5 f16 against the rounded oracle, 1e-3 against fp32) are sized for the
+    reference's shapes, whose wide windows average outputs down to |o| ~ 0.05.
+    Windows of a few keys here give |o| ~ 0.3-0.7, where one rounding of the
+    output alone costs ~1e-3 against fp32, and a correct kernel's error against
+    the rounded oracle is ~0.3 units of roundoff times |o|. So the rounded-oracle
+    mean may reach max(absolute, 0.75 u mean|o|) (u = 2^-8 bf16, 2^-11 f16),
+    and the fp32 mean may exceed the rounded oracle's own fp32 error by 1e-3.
+    `merged` (the LSE variant's teacher, two roundings) doubles the first."""
+    a = actual.float().cpu()
+    e32 = expected.float().cpu()
+    e = e32.to(dtype).float()
+    diff = (a - e).abs()
+    if dtype == torch.bfloat16:
+        atol, rtol, mean_limit = 8e-3, 1e-2, 4e-4
+    else:
+        atol, rtol, mean_limit = 2e-3, 5e-3, 6e-5
+    assert a.isfinite().all(), f"{what}: non-finite output"
+    bad = diff > atol + rtol * e.abs()
+    assert not bad.any(), (f"{what}: {bad.sum().item()} values exceed atol={atol}+rtol={rtol}; "
+                           f"max err {diff.max().item():.3g}")
+    limit = max(mean_limit, 0.75 * _unit_roundoff(dtype) * e.abs().mean().item())
+    limit *= 2 if merged else 1
+    assert diff.mean().item() <= limit, f"{what}: mean err {diff.mean().item():.3g} > {limit:.3g}"
+    d32 = (a - e32).abs()
+    assert d32.max().item() <= 2e-2, f"{what}: max err vs fp32 {d32.max().item():.3g}"
+    own = (e - e32).abs().mean().item()
+    assert d32.mean().item() <= 1e-3 + own, f"{what}: mean err vs fp32 {d32.mean().item():.3g}"
 
 
 def _case(i):
@@ -85,21 +124,5 @@ def test_random_shape_matches_oracle(gpu, i):
     if c["ws"] < wt:
         lo_t, _ = lse_dual_window_attn(qg, kg, vg, c["wt"], c["ws"])
         torch.cuda.synchronize()
-        _assert_merged_close(lo_t, rt, c["dtype"], f"case {i} LSE-variant teacher")
+        _assert_close(lo_t, rt, c["dtype"], f"case {i} LSE-variant teacher", merged=True)
 
-
-def _assert_merged_close(actual, expected, dtype, what):
-    """The LSE variant's teacher merges two outputs already rounded to the dtype
-    (profiling/lse_dual_attn.py:32-38 merges flash-attention's rounded outputs
-    the same way), so it carries two roundings: the pointwise bounds of
-    _assert_close, twice its mean bound, and the north-star bounds vs fp32."""
-    a = actual.float().cpu()
-    e32 = expected.float().cpu()
-    e = e32.to(dtype).float()
-    atol, rtol, mean_limit = (8e-3, 1e-2, 4e-4) if dtype == torch.bfloat16 else (2e-3, 5e-3, 6e-5)
-    diff = (a - e).abs()
-    assert a.isfinite().all(), f"{what}: non-finite output"
-    assert not (diff > atol + rtol * e.abs()).any(), f"{what}: max err {diff.max().item():.3g}"
-    assert diff.mean().item() <= 2 * mean_limit, f"{what}: mean err {diff.mean().item():.3g}"
-    d32 = (a - e32).abs()
-    assert d32.max().item() <= 2e-2 and d32.mean().item() <= 1e-3, what
