@@ -16,6 +16,12 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP) device")
 
 
+def random_cases(default: int) -> int:
+    """Case count of a seeded random sweep: `default`, times TTCD_RANDOM_SCALE when set
+    (a one-off deeper check over the same seeds plus more)."""
+    return max(1, int(default * float(os.environ.get("TTCD_RANDOM_SCALE", "1"))))
+
+
 def make_qkv(*, batch, seqlen, heads, kv_heads, head_dim, dtype=torch.bfloat16, seed=0,
              qk_scale=1.0, device="cuda"):
     """Seeded N(0,1) q, k, v drawn on the CPU in the order q, k, v, then moved to `device`

@@ -13,18 +13,17 @@ teachers, and unaligned values. Checks:
 """
 from __future__ import annotations
 
-import os
 import random
 
 import pytest
 import torch
 
+from conftest import random_cases
 from oracle import attn_ref
 
 pytestmark = pytest.mark.gpu
 
-# TTCD_RANDOM_CASES widens the sweep for a one-off deeper check (same seeds, more cases).
-N_CASES = int(os.environ.get("TTCD_RANDOM_CASES", "400"))
+N_CASES = random_cases(400)
 
 
 def _unit_roundoff(dtype):

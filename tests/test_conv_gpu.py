@@ -5,6 +5,8 @@ from __future__ import annotations
 import pytest
 import torch
 
+from conftest import random_cases
+
 from oracle import conv_ref
 
 pytestmark = pytest.mark.gpu
@@ -77,7 +79,7 @@ def _random_conv_case(i):
     return (b, nch, C, D), K, xdt, wdt
 
 
-@pytest.mark.parametrize("i", range(60))
+@pytest.mark.parametrize("i", range(random_cases(60)))
 @torch.inference_mode()
 def test_random_shapes_bitwise_vs_oracle(gpu, i):
     """Seeded random shapes (vector and scalar kernels, K up to 64, every dtype pair)

@@ -9,6 +9,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from conftest import random_cases
 from oracle import attn_ref, epilogue_ref
 from ttcd_amd import attn, epilogue
 
@@ -143,7 +144,7 @@ def test_headline_shape():
            y_t[:, rows], res_out[:, rows], y_s[:, rows])
 
 
-@pytest.mark.parametrize("i", range(30))
+@pytest.mark.parametrize("i", range(random_cases(30)))
 def test_random_shapes_match_oracle(i):
     """Seeded random batches, lengths, hidden sizes (multiples of 8 up to 2048) and
     dtype pairs against the oracle, with the bounds of test_matches_oracle."""

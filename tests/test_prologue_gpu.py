@@ -8,6 +8,8 @@ import types
 import pytest
 import torch
 
+from conftest import random_cases
+
 from oracle import attn_ref, prologue_ref
 from ttcd_amd import prologue
 
@@ -182,7 +184,7 @@ def _random_prologue_case(i):
                 base=r.choice([1e4, 1e5, 1e6]))
 
 
-@pytest.mark.parametrize("i", range(30))
+@pytest.mark.parametrize("i", range(random_cases(30)))
 def test_random_shapes_match_oracle(i):
     """Seeded random batches, lengths, head counts, head dims, dtypes, weight dtypes,
     positions and rotary bases against the oracle, with the bounds of test_matches_oracle."""

@@ -13,7 +13,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from conftest import make_qkv
+from conftest import make_qkv, random_cases
 from oracle import attn_ref
 
 pytestmark = pytest.mark.gpu
@@ -138,7 +138,7 @@ def _random_varlen_case(i):
     return lens, heads, kv_heads, D, wt, ws, dtype, r.random() < 0.3
 
 
-@pytest.mark.parametrize("i", range(40))
+@pytest.mark.parametrize("i", range(random_cases(40)))
 @torch.inference_mode()
 def test_random_varlen_equals_per_sequence_calls(gpu, i):
     """Seeded random packings, head shapes, windows and dtypes: every sequence
