@@ -9,7 +9,9 @@ teachers, and unaligned values. Checks:
     scaled to the output's magnitude, see _assert_close; LSE within 1e-3);
   * the LSE-combination variant's teacher against the same oracle (w_S < w_T),
     allowing for its second rounding;
-  * fused_dual_window_attn with exact_max=True against the oracle.
+  * fused_dual_window_attn with exact_max=True against the oracle;
+  * band_attn over random bands [lo, hi), rows with an empty band included
+    (o = 0, lse = -inf), in both rescale modes.
 """
 from __future__ import annotations
 
@@ -125,3 +127,31 @@ def test_random_shape_matches_oracle(gpu, i):
         torch.cuda.synchronize()
         _assert_close(lo_t, rt, c["dtype"], f"case {i} LSE-variant teacher", merged=True)
 
+
+
+@pytest.mark.parametrize("i", range(random_cases(100)))
+@torch.inference_mode()
+def test_random_band_matches_oracle(gpu, i):
+    """band_attn over a random band [lo, hi) (empty rows included: o = 0, lse = -inf),
+    on the shapes of _case, both rescale modes, against the oracle."""
+    from ttcd_amd import band_attn
+    c = _case(5000 + i)
+    r = random.Random(9000 + i)
+    lo = r.choice([0, r.randint(0, 300), r.randint(0, c["Tk"])])
+    hi = lo + r.choice([1, r.randint(1, 64), r.randint(1, c["Tk"] + 64)])
+    print(f"case {i}: {c} band [{lo}, {hi})", flush=True)
+    q, k, v = _inputs(c)
+    qg, kg, vg = q.cuda(), k.cuda(), v.cuda()
+    o, lse = band_attn(qg, kg, vg, lo, hi, return_lse=True)
+    xo = band_attn(qg, kg, vg, lo, hi, exact_max=True)
+    torch.cuda.synchronize()
+    ro, rl = _oracle(q, k, v, lo, hi)
+    empty = torch.isinf(rl)  # (B, H, Tq) rows with no key in the band
+    assert torch.equal(torch.isinf(lse.cpu()), empty), f"case {i}: -inf rows differ"
+    fin = ~empty
+    if fin.any():
+        assert (lse.cpu()[fin] - rl[fin]).abs().max().item() < 1e-3, f"case {i} lse"
+    rows_empty = empty.permute(0, 2, 1)  # (B, Tq, H)
+    assert (o.cpu()[rows_empty] == 0).all(), f"case {i}: empty rows not zero"
+    _assert_close(o, ro, c["dtype"], f"case {i} band")
+    _assert_close(xo, ro, c["dtype"], f"case {i} band exact_max")
