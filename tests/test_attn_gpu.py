@@ -226,6 +226,12 @@ def test_headline_shape_sampled_rows(gpu):
         _assert_close(out[:, rows], ro, torch.bfloat16, f"W={W}")
         assert (lse[:, :, rows].cpu() - rl).abs().max().item() < 1e-3
     assert math.isfinite(lt.float().sum().item())
+    # deterministic: no atomics or order-dependent reductions, so a second
+    # call gives the same bits
+    again = fused_dual_window_attn(q, k, v, WT, WS, return_lse=True)
+    torch.cuda.synchronize()
+    for a, b in zip((ot, os_, lt, ls), again):
+        assert torch.equal(a, b)
 
 
 @torch.inference_mode()
