@@ -389,6 +389,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-numerics", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--seqlen", type=int, default=32768, help="prompt length of --only e2e")
     ap.add_argument("--only", choices=["fused", "band", "lse", "conv", "copy", "prologue",
                                        "epilogue", "sweep", "e2e"],
                     help="profiling mode: run one workload --steps times and print its timing")
@@ -407,7 +408,8 @@ def main() -> int:
     if args.only == "e2e":
         with torch.inference_mode():
             print(json.dumps({"only": "e2e", **e2e_measure(args.steps, args.warmup,
-                                                            paths=("fused",))}), flush=True)
+                                                            T=args.seqlen, paths=("fused",))}),
+                  flush=True)
         return 0
     if args.only == "sweep":
         with torch.inference_mode():
