@@ -205,14 +205,16 @@ def test_forward_only_rejects_autograd_inputs(gpu):
         fused_dual_window_attn(q, k, v, -1, 192)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @torch.inference_mode()
-def test_headline_shape_sampled_rows(gpu):
+def test_headline_shape_sampled_rows(gpu, dtype):
     """Qwen3-0.6B 64K shape: the full-size run checked on sampled rows against the oracle,
     plus size-independent properties: finite outputs; rows whose teacher window holds no
     key beyond the student window (i < ws) give bit-identical teacher and student rows."""
     from ttcd_amd import fused_dual_window_attn
     T, WT, WS = 65536, 8192, 4096
-    q, k, v = make_qkv(batch=1, seqlen=T, heads=16, kv_heads=8, head_dim=128, seed=64)
+    q, k, v = make_qkv(batch=1, seqlen=T, heads=16, kv_heads=8, head_dim=128, seed=64,
+                       dtype=dtype)
     ot, os_, lt, ls = fused_dual_window_attn(q, k, v, WT, WS, return_lse=True)
     torch.cuda.synchronize()
     assert ot.isfinite().all() and os_.isfinite().all()
@@ -223,7 +225,7 @@ def test_headline_shape_sampled_rows(gpu):
     for W, out, lse in ((WT, ot, lt), (WS, os_, ls)):
         ro, rl = attn_ref.band_reference(q.cpu(), k.cpu(), v.cpu(), 0, W, rows=rows,
                                          return_lse=True)
-        _assert_close(out[:, rows], ro, torch.bfloat16, f"W={W}")
+        _assert_close(out[:, rows], ro, dtype, f"W={W}")
         assert (lse[:, :, rows].cpu() - rl).abs().max().item() < 1e-3
     assert math.isfinite(lt.float().sum().item())
     # deterministic: no atomics or order-dependent reductions, so a second
