@@ -16,19 +16,30 @@ pytestmark = pytest.mark.gpu
 
 
 @torch.inference_mode()
-def test_dual_window_and_conv_replays_equal_eager(gpu):
-    from ttcd_amd import causal_dwconv_x, fused_dual_window_attn, fused_dual_window_attn_varlen
+def test_hot_path_replays_equal_eager(gpu):
+    from ttcd_amd import (causal_dwconv_x, epilogue, fused_dual_window_attn,
+                          fused_dual_window_attn_varlen, lse_dual_window_attn, prologue)
     B, T, H, HK, D, wt, ws = 1, 1000, 8, 4, 128, 384, 130
     q, k, v = make_qkv(batch=B, seqlen=T, heads=H, kv_heads=HK, head_dim=D, seed=1)
     x = torch.randn(2, 3, 64, 256, device="cuda").to(torch.bfloat16)
     w = torch.randn(256, 5, device="cuda").to(torch.bfloat16)
     cu = torch.tensor([0, 300, 301, 1000], dtype=torch.int32, device="cuda")
     qp, kp, vp = q[0], k[0], v[0]
+    wq = torch.randn(D, device="cuda").to(torch.bfloat16)
+    wk = torch.randn(D, device="cuda").to(torch.bfloat16)
+    cos, sin = prologue.rope_tables(prologue.rope_inv_freq(D, 1e6, "cuda"), T, torch.bfloat16)
+    hid = H * D
+    res = torch.randn(B, T, hid, device="cuda").to(torch.bfloat16)
+    wn = torch.randn(hid, device="cuda").to(torch.bfloat16)
 
     def step():
         ot, os_, lt, ls = fused_dual_window_attn(q, k, v, wt, ws, return_lse=True)
         vt, vs = fused_dual_window_attn_varlen(qp, kp, vp, cu, 700, wt, ws)
-        return ot, os_, lt, ls, vt, vs, causal_dwconv_x(x, w)
+        lt_, ls_ = lse_dual_window_attn(q, k, v, wt, ws)
+        pq, pk = prologue.qk_norm_rope(q, k, wq, wk, 1e-6, cos, sin, 0)
+        ep = epilogue.dual_residual_rmsnorm(ot.reshape(B, T, hid), os_.reshape(B, T, hid), res,
+                                            wn, 1e-6)
+        return (ot, os_, lt, ls, vt, vs, causal_dwconv_x(x, w), lt_, ls_, pq, pk, *ep)
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -41,7 +52,7 @@ def test_dual_window_and_conv_replays_equal_eager(gpu):
     g = torch.Generator(device="cuda")
     for rep in range(3):
         g.manual_seed(100 + rep)
-        for t in (q, k, v, x):
+        for t in (q, k, v, x, res):
             t.copy_(torch.randn(t.shape, generator=g, device="cuda").to(t.dtype))
         graph.replay()
         torch.cuda.synchronize()
