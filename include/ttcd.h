@@ -17,6 +17,7 @@
 #ifndef TTCD_H_
 #define TTCD_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -95,7 +96,10 @@ ttcd_status ttcd_band_attn_fwd(
  * the reference kernel (fused_dual_attn.py:100-107), whose numerics it then
  * follows: at config 1, 98.6 % (teacher) and 99.96 % (student) of the bf16
  * outputs are bit-identical to a CPU emulation of the reference kernel, vs
- * 58-61 % at 8, for ~5 % more time. Must lie in [0, 16].
+ * 58-61 % at 8, for ~5 % more time. Must lie in [0, 16] for BF16 and in
+ * [0, 15] for F16 (probabilities reach 2^rescale_log2 and are rounded to the
+ * input dtype before PV; f16 overflows at 65520), else
+ * TTCD_ERR_INVALID_ARGUMENT.
  *
  * Cached prefill (Tq <= Tk): the same two calls for Tq new query rows against
  * Tk keys, the queries at absolute positions Tk - Tq .. Tk - 1 (the bottom-
@@ -172,6 +176,35 @@ ttcd_status ttcd_lse_merge_fwd(const void* o_s, const float* lse_s,
                                int B, int T, int H, int D, int row_start,
                                const int64_t o_stride[4], ttcd_dtype dtype,
                                void* stream);
+
+/*
+ * The LSE-combination variant in one call: o_s = the window_s call, o_t =
+ * the exact log-sum-exp merge of o_s with the far band window_s <= i-j <
+ * window_t. Replaces lse_dual_window_attn_fa3_fast (and
+ * lse_dual_window_attn / _fa3, which compute the same thing;
+ * profiling/lse_dual_attn.py:16-39, :74-99, :134-160), including its
+ * o_t[:, :WS] = o_s[:, :WS] rows. Queries are the last Tq of Tk positions as
+ * in the kv forms (Tq == Tk for a fresh prefill). Requires
+ * 1 <= window_s < window_t (window_t < 0: full causal), as the reference
+ * asserts (lse_dual_attn.py:20). Other arguments as in
+ * ttcd_dual_window_attn_kv_fwd.
+ * workspace: device scratch for the far-band partial and both LSEs,
+ * 256-byte aligned. With workspace_bytes >=
+ * ttcd_lse_dual_window_attn_workspace_bytes(...) the rows run in one pass;
+ * a smaller workspace runs them in chunks that fit (same results, bit for
+ * bit); TTCD_ERR_INVALID_ARGUMENT if it holds no row. The workspace is not
+ * read before it is written and may be reused once the stream has passed
+ * the call.
+ */
+size_t ttcd_lse_dual_window_attn_workspace_bytes(int B, int Tq, int Tk, int Hq, int D,
+                                                 int window_s);
+ttcd_status ttcd_lse_dual_window_attn_fwd(
+    const void* q, const void* k, const void* v, void* o_t, void* o_s,
+    int B, int Tq, int Tk, int Hq, int Hkv, int D,
+    const int64_t q_stride[4], const int64_t k_stride[4],
+    const int64_t v_stride[4], const int64_t o_stride[4],
+    int window_t, int window_s, float sm_scale, float rescale_log2,
+    ttcd_dtype dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Chunk-local causal depthwise conv along C on the (N, C, D) layout.

@@ -162,3 +162,23 @@ def test_kv_calls_reject_rescale_threshold(rescale):
         p, p, p, p, None, 1, 64, 64, 4, 2, 64, qs, ks, ks, qs, 0, 32, 0.125, rescale,
         _lib.DTYPE_BF16, None) == _lib.TTCD_ERR_INVALID_ARGUMENT
     assert b"rescale_log2" in lib.ttcd_last_error()
+
+
+@pytest.mark.parametrize("rescale", [15.5, 16.0])
+def test_f16_rescale_threshold_bounded_by_f16_range(rescale):
+    """Under the lazy max a probability reaches 2^rescale_log2 and is rounded to
+    the input dtype before PV; f16 rounds values >= 65520 to +inf, so F16 calls
+    take at most 15 (bf16 keeps 16)."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x10000)
+    qs = _lib.strides4([64 * 4 * 64, 4 * 64, 64, 1])
+    ks = _lib.strides4([64 * 2 * 64, 2 * 64, 64, 1])
+    assert lib.ttcd_dual_window_attn_kv_fwd(
+        p, p, p, p, p, None, None, 1, 64, 64, 4, 2, 64, qs, ks, ks, qs, 32, 16, 0.125, rescale,
+        _lib.DTYPE_F16, None) == _lib.TTCD_ERR_INVALID_ARGUMENT
+    assert b"rescale_log2" in lib.ttcd_last_error()
+    assert lib.ttcd_band_attn_kv_fwd(
+        p, p, p, p, None, 1, 64, 64, 4, 2, 64, qs, ks, ks, qs, 0, 32, 0.125, rescale,
+        _lib.DTYPE_F16, None) == _lib.TTCD_ERR_INVALID_ARGUMENT
+    assert _varlen_call("dual", dtype=_lib.DTYPE_F16, rescale=rescale) == \
+        _lib.TTCD_ERR_INVALID_ARGUMENT

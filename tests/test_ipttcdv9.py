@@ -186,7 +186,9 @@ def test_resolve_config_and_unsupported_options():
     # modeling_ipttcdv9.py:98-102: 256 * ceil(1024 * 4 * 2 / 3 / 256)
     assert derived["intermediate_size"] == 2816 and derived["head_dim"] == 64
     for bad in ({"use_output_gate": True}, {"ttt_weight_renorm": True}, {"use_muon": True},
-                {"ttt_normalize_student_features": True}, {"qkv_bias": True}):
+                {"ttt_normalize_student_features": True}, {"qkv_bias": True},
+                {"fuse_norm": False}, {"ttt_scan_state_dtype": "fp32"},
+                {"ttt_scan_state_dtype": "BF16"}):
         with pytest.raises(NotImplementedError):
             M.resolve_config(dict(M.QWEN3_06B_SWA8K, **bad))
 

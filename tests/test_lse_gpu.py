@@ -75,3 +75,55 @@ def test_merge_kernel(gpu):
     assert torch.equal(out[:, 100:110], o_s[:, 100:110])
     rep = attn_ref.ulp_report(out[:, 50:], ref[:, 50:])
     assert rep["max_ulp"] <= 1 and rep["bit_equal_pct"] > 97.0, rep
+
+
+def lse_variant_c(q, k, v, wt, ws, workspace_bytes=None, exact_max=False):
+    """ttcd_lse_dual_window_attn_fwd through the C ABI with a workspace of
+    `workspace_bytes` (None: the one-pass size)."""
+    from ttcd_amd import _lib
+    L = _lib.lib()
+    B, Tq, H, D = q.shape
+    Tk, HK = k.shape[1], k.shape[2]
+    need = L.ttcd_lse_dual_window_attn_workspace_bytes(B, Tq, Tk, H, D, ws)
+    nbytes = need if workspace_bytes is None else workspace_bytes
+    wsb = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    ot = torch.empty_like(q)
+    os_ = torch.empty_like(q)
+    dt = _lib.DTYPE_BF16 if q.dtype == torch.bfloat16 else _lib.DTYPE_F16
+    _lib.check(L.ttcd_lse_dual_window_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), ot.data_ptr(), os_.data_ptr(), B, Tq, Tk, H, HK,
+        D, _lib.strides4(q.stride()), _lib.strides4(k.stride()), _lib.strides4(v.stride()),
+        _lib.strides4(ot.stride()), wt, ws, D ** -0.5, 0.0 if exact_max else 8.0, dt,
+        wsb.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream))
+    return ot, os_, need
+
+
+@pytest.mark.parametrize("B,Tq,Tk,H,HK,D,wt,ws,dtype", [
+    (1, 1500, 1500, 8, 4, 128, 700, 300, torch.bfloat16),
+    (2, 1000, 1000, 15, 5, 64, -1, 257, torch.float16),
+    (1, 700, 1300, 4, 2, 128, 900, 128, torch.bfloat16),   # cached prefill, Tq < Tk
+    (3, 333, 333, 6, 3, 64, 200, 199, torch.bfloat16),
+])
+@torch.inference_mode()
+def test_lse_variant_chunked_workspace_is_bitwise(gpu, B, Tq, Tk, H, HK, D, wt, ws, dtype):
+    """A workspace smaller than the one-pass size runs the far-band rows in
+    chunks; every row's result depends only on its absolute position, so the
+    outputs are bit-identical to the one-pass call, and the one-pass call
+    matches the oracle."""
+    g = torch.Generator().manual_seed(B * 1000 + Tq)
+    q = torch.randn(B, Tq, H, D, generator=g).to(dtype).to(gpu)
+    k = torch.randn(B, Tk, HK, D, generator=g).to(dtype).to(gpu)
+    v = torch.randn(B, Tk, HK, D, generator=g).to(dtype).to(gpu)
+    ot, os_, need = lse_variant_c(q, k, v, wt, ws)
+    per_row = B * H * (2 * D + 8)
+    for rows in (1, 100, 300):
+        ct, cs, _ = lse_variant_c(q, k, v, wt, ws, workspace_bytes=rows * per_row + 768)
+        assert torch.equal(ct, ot) and torch.equal(cs, os_), rows
+    W = Tk if wt < 0 else wt
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    # the oracle aligns the Tq queries bottom-right against the Tk keys
+    rt = attn_ref.dense_reference(qc, kc, vc, W)
+    rs = attn_ref.dense_reference(qc, kc, vc, ws)
+    _assert_close(ot, rt, dtype, "teacher")
+    _assert_close(os_, rs, dtype, "student")
+    assert torch.equal(os_, __import__("ttcd_amd").window_attn(q, k, v, ws))

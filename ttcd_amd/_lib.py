@@ -36,6 +36,8 @@ EXPORTS = (
     "ttcd_dual_window_attn_varlen_fwd",
     "ttcd_band_attn_varlen_fwd",
     "ttcd_lse_merge_fwd",
+    "ttcd_lse_dual_window_attn_workspace_bytes",
+    "ttcd_lse_dual_window_attn_fwd",
     "ttcd_causal_dwconv_chunked_fwd",
     "ttcd_qk_norm_rope_fwd",
     "ttcd_rope_table_fwd",
@@ -91,6 +93,13 @@ _SIGS = {
     "ttcd_lse_merge_fwd": (_i32, [
         _vp, _fp, _vp, _fp, _vp,
         _i32, _i32, _i32, _i32, _i32, _i64x4, _i32, _vp]),
+    "ttcd_lse_dual_window_attn_workspace_bytes": (ctypes.c_size_t, [
+        _i32, _i32, _i32, _i32, _i32, _i32]),
+    "ttcd_lse_dual_window_attn_fwd": (_i32, [
+        _vp, _vp, _vp, _vp, _vp,
+        _i32, _i32, _i32, _i32, _i32, _i32,
+        _i64x4, _i64x4, _i64x4, _i64x4,
+        _i32, _i32, ctypes.c_float, ctypes.c_float, _i32, _vp, ctypes.c_size_t, _vp]),
     "ttcd_causal_dwconv_chunked_fwd": (_i32, [
         _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp]),
     "ttcd_qk_norm_rope_fwd": (_i32, [

@@ -302,19 +302,33 @@ def lse_dual_window_attn(q, k, v, window_teacher: int, window_student: int, *,
                          exact_max: bool = False):
     """Student = window WS (with LSE); far band [WS, WT) (with LSE); teacher =
     exact LSE merge. profiling/lse_dual_attn.py:16-39 (flash-attn there, the
-    gfx950 band kernel here). Requires WS < WT (AssertionError otherwise)."""
+    gfx950 band kernel here). Requires WS < WT (AssertionError otherwise).
+    One C call (ttcd_lse_dual_window_attn_fwd) with the far-band partial and
+    both LSEs in a workspace allocated here; k / v may be longer than q (the
+    queries are then the last Tq positions, as in fused_dual_window_attn)."""
     B, Tq, H, D = q.shape
     Tk = k.shape[1]
     WT = Tk if (window_teacher is None or window_teacher < 0) else window_teacher
     WS = window_student
     assert WS < WT
-    o_s, lse_s = window_attn(q, k, v, WS, return_lse=True, exact_max=exact_max)
     if Tk <= WS:
+        o_s = window_attn(q, k, v, WS, exact_max=exact_max)
         return o_s, o_s
-    o_f, lse_f = band_attn(q, k, v, WS, WT, return_lse=True, exact_max=exact_max)
-    # rows at absolute positions below WS have an empty far band
-    o_t = lse_merge(o_s, lse_s, o_f, lse_f, row_start=max(0, WS - (Tk - Tq)))
-    return o_t, o_s
+    B, Tq, H, HK, D = _check_qkv(q, k, v, "lse_dual_window_attn")
+    q, k, v = _ready(q), _ready(k), _ready(v)
+    # o_t and o_s as the halves of one allocation (see fused_dual_window_attn)
+    both = torch.empty((2,) + tuple(q.shape), dtype=q.dtype, device=q.device)
+    ot, os_ = both[0], both[1]
+    L = _lib.lib()
+    WS_ = int(min(WS, 2**31 - 1))
+    nbytes = L.ttcd_lse_dual_window_attn_workspace_bytes(B, Tq, Tk, H, D, WS_)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=q.device)
+    _lib.check(L.ttcd_lse_dual_window_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), ot.data_ptr(), os_.data_ptr(), B, Tq, Tk, H,
+        HK, D, _lib.strides4(q.stride()), _lib.strides4(k.stride()), _lib.strides4(v.stride()),
+        _lib.strides4(ot.stride()), int(min(WT, 2**31 - 1)), WS_, D ** -0.5,
+        _rescale(exact_max), _DT[q.dtype], ws.data_ptr(), int(nbytes), _stream(q.device)))
+    return ot, os_
 
 
 def lse_dual_window_attn_fa3(q, k, v, window_teacher: int, window_student: int):

@@ -75,12 +75,15 @@ ttcd_status check_attn(const void* q, const void* k, const void* v, const void* 
   return TTCD_OK;
 }
 
-// The lazy-rescale threshold: finite, 0 (exact running max) .. 16 (keeps every
-// probability below 2^16 times its row's largest, far from fp32 overflow).
-ttcd_status check_rescale(float rescale_log2) {
-  if (!(rescale_log2 >= 0.f && rescale_log2 <= 16.f))
-    return fail(TTCD_ERR_INVALID_ARGUMENT, "rescale_log2 must be in [0, 16] (got %g)",
-                (double)rescale_log2);
+// The lazy-rescale threshold: finite, 0 (exact running max) .. 16. Every
+// probability p = exp2(s*c - m*c) stays <= 2^rescale_log2 and is rounded to
+// the input dtype before PV: bf16 holds any such p, but f16 rounds values
+// >= 65520 to +inf, so F16 is limited to 15 (p <= 32768).
+ttcd_status check_rescale(float rescale_log2, ttcd_dtype dtype) {
+  const float hi = dtype == TTCD_DTYPE_F16 ? 15.f : 16.f;
+  if (!(rescale_log2 >= 0.f && rescale_log2 <= hi))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "rescale_log2 must be in [0, %g] for this dtype (got %g)",
+                (double)hi, (double)rescale_log2);
   return TTCD_OK;
 }
 
@@ -163,7 +166,7 @@ ttcd_status ttcd_dual_window_attn_kv_fwd(const void* q, const void* k, const voi
                                          float rescale_log2, ttcd_dtype dtype, void* stream) {
   ttcd_status st =
       check_attn(q, k, v, o_t, B, Tk, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
-  if (st == TTCD_OK) st = check_rescale(rescale_log2);
+  if (st == TTCD_OK) st = check_rescale(rescale_log2, dtype);
   if (st != TTCD_OK) return st;
   if (!o_s) return fail(TTCD_ERR_INVALID_ARGUMENT, "null student output pointer");
   if (!aligned16(o_s)) return fail(TTCD_ERR_UNSUPPORTED, "o_s must be 16-byte aligned");
@@ -207,7 +210,7 @@ ttcd_status ttcd_band_attn_kv_fwd(const void* q, const void* k, const void* v, v
                                   ttcd_dtype dtype, void* stream) {
   ttcd_status st =
       check_attn(q, k, v, o, B, Tk, Hq, Hkv, D, q_stride, k_stride, v_stride, o_stride, dtype);
-  if (st == TTCD_OK) st = check_rescale(rescale_log2);
+  if (st == TTCD_OK) st = check_rescale(rescale_log2, dtype);
   if (st != TTCD_OK) return st;
   if (band_lo < 0 || band_hi <= band_lo)
     return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi (got %d, %d)", band_lo,
@@ -249,7 +252,7 @@ static ttcd_status varlen_args(ttcd::AttnArgs* a, const void* q, const void* k, 
                                const int64_t* os3, float sm_scale, float rescale_log2,
                                ttcd_dtype dtype) {
   if (!cu_seqlens) return fail(TTCD_ERR_INVALID_ARGUMENT, "null cu_seqlens");
-  if (check_rescale(rescale_log2) != TTCD_OK) return TTCD_ERR_INVALID_ARGUMENT;
+  if (check_rescale(rescale_log2, dtype) != TTCD_OK) return TTCD_ERR_INVALID_ARGUMENT;
   if (!qs3 || !ks3 || !vs3 || !os3) return fail(TTCD_ERR_INVALID_ARGUMENT, "null stride array");
   if (nseq < 1 || max_seqlen < 1 || total < 0)
     return fail(TTCD_ERR_INVALID_ARGUMENT,
@@ -346,10 +349,163 @@ ttcd_status ttcd_lse_merge_fwd(const void* o_s, const float* lse_s, const void* 
   if (!aligned16(o_s) || !aligned16(o_f) || !aligned16(o_t))
     return fail(TTCD_ERR_UNSUPPORTED, "outputs must be 16-byte aligned");
   if (row_start < 0) return fail(TTCD_ERR_INVALID_ARGUMENT, "row_start must be >= 0");
-  return from_hip(ttcd::launch_lse_merge(o_s, lse_s, o_f, lse_f, o_t, B, T, H, D, row_start,
-                                         o_stride[0], o_stride[1], o_stride[2], elem(dtype),
-                                         static_cast<hipStream_t>(stream)),
+  ttcd::MergeArgs m = {o_s, lse_s, o_f, lse_f, o_t, B, T, H, D, row_start,
+                       o_stride[0], o_stride[1], o_stride[2],
+                       o_stride[0], o_stride[1], o_stride[2]};
+  return from_hip(ttcd::launch_lse_merge(m, elem(dtype), static_cast<hipStream_t>(stream)),
                   "lse merge launch");
+}
+
+// ---------------------------------------------------------------------------
+// The LSE-combination variant as one call (lse_dual_window_attn_fa3_fast,
+// profiling/lse_dual_attn.py:134-160, with the cached-prefill rows of the kv
+// forms). Query rows whose absolute position is below window_s have an empty
+// far band: they are one student call, copied to o_t. The other rows run in
+// chunks that fit the scratch: per chunk a student call (o_s rows + lse_s),
+// a far-band call (o_f + lse_f) and the merge into o_t. Each row's tiles,
+// order and arithmetic depend only on its absolute position, so the result
+// does not depend on the chunking.
+namespace {
+
+constexpr size_t kScratchAlign = 256;
+size_t align_up(size_t x) { return (x + kScratchAlign - 1) & ~(kScratchAlign - 1); }
+
+struct LseDual {
+  const void *q, *k, *v;
+  void *o_t, *o_s;
+  int B, Tq, Tk, Hq, Hkv, D, WT, WS;
+  const int64_t *qs, *ks, *vs, *os;
+  float sm_scale, rescale_log2;
+  ttcd_dtype dtype;
+  int esize() const { return 2; }
+  // first query row with a far band (absolute position >= WS)
+  int n0() const {
+    const int r = WS - (Tk - Tq);
+    return r < 0 ? 0 : (r > Tq ? Tq : r);
+  }
+  // scratch of a chunk of `rows` rows: o_f (B, rows, Hq, D), lse_s and lse_f (B, Hq, rows)
+  size_t chunk_bytes(int64_t rows) const {
+    return align_up((size_t)B * rows * Hq * D * esize()) + 2 * align_up((size_t)B * Hq * rows * 4);
+  }
+  // most rows per chunk that `bytes` of scratch hold (a multiple of the
+  // 128-row query block when at least one block fits); 0 if not even one row
+  int64_t rows_fitting(size_t bytes) const {
+    const int64_t need = Tq - n0();
+    if (need <= 0) return 1;
+    if (chunk_bytes(need) <= bytes) return need;
+    const size_t per_row = (size_t)B * Hq * (D * esize() + 8);
+    int64_t r = bytes > 3 * kScratchAlign ? (int64_t)((bytes - 3 * kScratchAlign) / per_row) : 0;
+    while (r > 0 && chunk_bytes(r) > bytes) --r;
+    if (r >= ttcd::kBlockM) r -= r % ttcd::kBlockM;
+    return r;
+  }
+};
+
+// Window and pointer checks of the LSE variant (the band calls check the rest).
+ttcd_status check_lse_dual(LseDual* a, int window_t, int window_s) {
+  if (!a->q || !a->k || !a->v || !a->o_t || !a->o_s)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null tensor pointer");
+  if (!a->qs || !a->ks || !a->vs || !a->os)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null stride array");
+  if (a->B < 1 || a->Tq < 1 || a->Tq > a->Tk || a->Hq < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need B >= 1, Hq >= 1, 1 <= Tq <= Tk (got %d, %d, %d, %d)",
+                a->B, a->Hq, a->Tq, a->Tk);
+  if (a->dtype != TTCD_DTYPE_BF16 && a->dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "attention dtype must be bf16 or f16");
+  if (window_t < 0) window_t = a->Tk;
+  if (window_s < 1) return fail(TTCD_ERR_INVALID_ARGUMENT, "window_s must be >= 1 (got %d)", window_s);
+  // lse_dual_attn.py:20: the far band [WS, WT) must not be empty
+  if (window_s >= window_t)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "window_s (%d) must be < window_t (%d)", window_s,
+                window_t);
+  if (!aligned16(a->o_t) || !aligned16(a->o_s))
+    return fail(TTCD_ERR_UNSUPPORTED, "outputs must be 16-byte aligned");
+  a->WT = window_t;
+  a->WS = window_s;
+  return TTCD_OK;
+}
+
+// Run the variant with `ws_bytes` of device scratch at `ws` (256-byte aligned).
+ttcd_status run_lse_dual(const LseDual& a, char* ws, size_t ws_bytes, void* stream) {
+  const int qoff = a.Tk - a.Tq, n0 = a.n0();
+  const int64_t rows = a.rows_fitting(ws_bytes);
+  if (n0 < a.Tq && rows < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "scratch of %zu bytes holds no query row (need %zu)",
+                ws_bytes, a.chunk_bytes(1));
+  const size_t es = a.esize();
+  const char* q = static_cast<const char*>(a.q);
+  char* o_s = static_cast<char*>(a.o_s);
+  char* o_t = static_cast<char*>(a.o_t);
+  const ttcd::Elem et = elem(a.dtype);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  ttcd_status st;
+  if (n0 > 0) {
+    // rows below WS: the student call alone; o_t = o_s
+    st = ttcd_band_attn_kv_fwd(a.q, a.k, a.v, a.o_s, nullptr, a.B, n0, qoff + n0, a.Hq, a.Hkv,
+                               a.D, a.qs, a.ks, a.vs, a.os, 0, a.WS, a.sm_scale, a.rescale_log2,
+                               a.dtype, stream);
+    if (st != TTCD_OK) return st;
+    ttcd::MergeArgs m = {a.o_s, nullptr, a.o_s, nullptr, a.o_t, a.B, n0, a.Hq, a.D, n0,
+                         a.os[0], a.os[1], a.os[2], a.os[0], a.os[1], a.os[2]};
+    st = from_hip(ttcd::launch_lse_merge(m, et, hs), "lse variant copy launch");
+    if (st != TTCD_OK) return st;
+  }
+  for (int64_t r0 = n0; r0 < a.Tq; r0 += rows) {
+    const int r1 = (int)(r0 + rows < a.Tq ? r0 + rows : a.Tq);
+    const int tc = r1 - (int)r0, tk = qoff + r1;
+    char* o_f = ws;
+    float* lse_s = reinterpret_cast<float*>(ws + align_up((size_t)a.B * tc * a.Hq * a.D * es));
+    float* lse_f = reinterpret_cast<float*>(reinterpret_cast<char*>(lse_s) +
+                                            align_up((size_t)a.B * a.Hq * tc * 4));
+    const int64_t fs[4] = {(int64_t)tc * a.Hq * a.D, (int64_t)a.Hq * a.D, a.D, 1};
+    const void* qc = q + (size_t)r0 * a.qs[1] * es;
+    void* osc = o_s + (size_t)r0 * a.os[1] * es;
+    st = ttcd_band_attn_kv_fwd(qc, a.k, a.v, osc, lse_s, a.B, tc, tk, a.Hq, a.Hkv, a.D, a.qs,
+                               a.ks, a.vs, a.os, 0, a.WS, a.sm_scale, a.rescale_log2, a.dtype,
+                               stream);
+    if (st != TTCD_OK) return st;
+    st = ttcd_band_attn_kv_fwd(qc, a.k, a.v, o_f, lse_f, a.B, tc, tk, a.Hq, a.Hkv, a.D, a.qs,
+                               a.ks, a.vs, fs, a.WS, a.WT, a.sm_scale, a.rescale_log2, a.dtype,
+                               stream);
+    if (st != TTCD_OK) return st;
+    ttcd::MergeArgs m = {osc, lse_s, o_f, lse_f, o_t + (size_t)r0 * a.os[1] * es, a.B, tc, a.Hq,
+                         a.D, 0, a.os[0], a.os[1], a.os[2], fs[0], fs[1], fs[2]};
+    st = from_hip(ttcd::launch_lse_merge(m, et, hs), "lse variant merge launch");
+    if (st != TTCD_OK) return st;
+  }
+  return ok();
+}
+
+}  // namespace
+
+size_t ttcd_lse_dual_window_attn_workspace_bytes(int B, int Tq, int Tk, int Hq, int D,
+                                                 int window_s) {
+  if (B < 1 || Tq < 1 || Tq > Tk || Hq < 1 || D < 1 || window_s < 1) return 0;
+  LseDual a = {};
+  a.B = B;
+  a.Tq = Tq;
+  a.Tk = Tk;
+  a.Hq = Hq;
+  a.D = D;
+  a.WS = window_s;
+  const int64_t need = Tq - a.n0();
+  return need > 0 ? a.chunk_bytes(need) : 0;
+}
+
+ttcd_status ttcd_lse_dual_window_attn_fwd(const void* q, const void* k, const void* v,
+                                          void* o_t, void* o_s, int B, int Tq, int Tk, int Hq,
+                                          int Hkv, int D, const int64_t q_stride[4],
+                                          const int64_t k_stride[4], const int64_t v_stride[4],
+                                          const int64_t o_stride[4], int window_t, int window_s,
+                                          float sm_scale, float rescale_log2, ttcd_dtype dtype,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  LseDual a = {q, k, v, o_t, o_s, B, Tq, Tk, Hq, Hkv, D, 0, 0, q_stride, k_stride, v_stride,
+               o_stride, sm_scale, rescale_log2, dtype};
+  ttcd_status st = check_lse_dual(&a, window_t, window_s);
+  if (st != TTCD_OK) return st;
+  if (workspace_bytes > 0 && (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u)))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "workspace must be non-null and 256-byte aligned");
+  return run_lse_dual(a, static_cast<char*>(workspace), workspace_bytes, stream);
 }
 
 ttcd_status ttcd_causal_dwconv_chunked_fwd(const void* x, const void* w, void* y, int64_t N,

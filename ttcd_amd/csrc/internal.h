@@ -105,9 +105,17 @@ hipError_t launch_ttt_features(const TttFeatureArgs& a, Elem dtype, Elem w_dtype
 hipError_t launch_dwconv(const void* x, const void* w, void* y, int64_t N, int C,
                          int D, int K, Elem xt, Elem wt, hipStream_t stream);
 
-hipError_t launch_lse_merge(const void* o_s, const float* lse_s, const void* o_f,
-                            const float* lse_f, void* o_t, int B, int T, int H,
-                            int D, int row_start, int64_t sb, int64_t st,
-                            int64_t sh, Elem dtype, hipStream_t stream);
+// Log-sum-exp merge of two partials (merge.hip). Rows t < row_start copy o_s.
+struct MergeArgs {
+  const void* o_s;      // (B, T, H, D), strides sb / st / sh (o_t shares them)
+  const float* lse_s;   // (B, H, T) contiguous
+  const void* o_f;      // (B, T, H, D), strides f_sb / f_st / f_sh
+  const float* lse_f;   // (B, H, T) contiguous
+  void* o_t;
+  int B, T, H, D, row_start;
+  int64_t sb, st, sh;
+  int64_t f_sb, f_st, f_sh;
+};
+hipError_t launch_lse_merge(const MergeArgs& a, Elem dtype, hipStream_t stream);
 
 }  // namespace ttcd

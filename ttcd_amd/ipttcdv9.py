@@ -82,7 +82,8 @@ _DEFAULTS = {
     "ttt_output_use_teacher_conv": True, "ttt_output_source": "teacher", "dynamic_lr": True,
     "ttt_visible_chunks": 1, "use_muon": False, "ttt_weight_renorm": False,
     "ttt_norm_proj_diff": False, "ttt_normalize_student_features": True,
-    "ttt_update_every": 4, "ttt_fuse_proj_into_update": True,
+    "ttt_update_every": 4, "ttt_fuse_proj_into_update": True, "fuse_norm": True,
+    "ttt_scan_state_dtype": "compute",
 }
 
 
@@ -110,7 +111,13 @@ def resolve_config(cfg: dict) -> dict:
         ("ttt_norm_proj_diff", c["ttt_norm_proj_diff"]),
         ("ttt_output_use_teacher_conv", c["ttt_layers"] and c["ttt_output_use_teacher_conv"]),
         ("ttt_output_source", c["ttt_output_source"] != "teacher"),
-        ("ttt_fuse_proj_into_update=False", not c["ttt_fuse_proj_into_update"])) if bad]
+        ("ttt_fuse_proj_into_update=False", not c["ttt_fuse_proj_into_update"]),
+        # nn.RMSNorm with a rounded residual add (configuration_ipttcd.py:37, 89)
+        ("fuse_norm=False", not c["fuse_norm"]),
+        # an fp32 or bf16 scan state instead of the compute dtype
+        # (configuration_ipttcdv9.py:17-34, modeling_ipttcdv9.py:180-181)
+        ("ttt_scan_state_dtype", str(c["ttt_scan_state_dtype"]).lower() != "compute"),
+    ) if bad]
     if unsupported:
         raise NotImplementedError(f"ipttcdv9 prefill: unsupported options {unsupported}")
     return c

@@ -94,28 +94,33 @@ def ttt_features(gu_t: torch.Tensor, gu_s: torch.Tensor, conv_t: torch.Tensor | 
     None. Returns (z, z_hat, diff): z (rows, I) teacher features, z_hat the
     student's after its conv, diff = conv_t(z) - z_hat for every chunk but the
     last of each batch row, (B*(nchunk-1)*chunk, I)."""
-    _check_gpu("ttt_features", gu_t=gu_t, gu_s=gu_s, conv_t=conv_t, conv_s=conv_s)
     rows = B * nchunk * chunk
     if gu_t.shape != gu_s.shape or gu_t.dim() != 2 or gu_t.shape[0] != rows:
         raise ValueError(f"ttt_features: gate|up must be ({rows}, 2*I), got {tuple(gu_t.shape)}")
     if gu_t.stride() != gu_s.stride() or gu_t.stride(1) != 1:
         raise ValueError("ttt_features: teacher and student gate|up must share a row stride")
     I = gu_t.shape[1] // 2
+    # Every present weight must have the first present weight's kernel size:
+    # the kernel reads K taps of each, so a shorter one would be over-read.
     ws = []
-    K = 1
+    K = None
     for w in (conv_t, conv_s):
         if w is None:
             ws.append(None)
             continue
-        w2 = w.reshape(w.shape[0], -1).contiguous()
+        w2 = w.reshape(w.shape[0], -1)
         if w2.shape[0] != I:
             raise ValueError(f"ttt_features: conv weight must be ({I}, K)")
-        if K != 1 and w2.shape[1] != K:
+        if K is not None and w2.shape[1] != K:
             raise ValueError("ttt_features: both convs must share a kernel size")
         K = w2.shape[1]
         ws.append(w2)
+    if K is None:
+        K = 1
     if ws[0] is not None and ws[1] is not None and ws[0].dtype != ws[1].dtype:
         raise ValueError("ttt_features: both conv weights must share a dtype")
+    _check_gpu("ttt_features", gu_t=gu_t, gu_s=gu_s, conv_t=conv_t, conv_s=conv_s)
+    ws = [w.contiguous() if w is not None else None for w in ws]
     wdt = next((w.dtype for w in ws if w is not None), torch.float32)
     dev, dt = gu_t.device, gu_t.dtype
     z = torch.empty(rows, I, dtype=dt, device=dev)
