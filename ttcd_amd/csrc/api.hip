@@ -420,6 +420,13 @@ ttcd_status check_lse_dual(LseDual* a, int window_t, int window_s) {
                 window_t);
   if (!aligned16(a->o_t) || !aligned16(a->o_s))
     return fail(TTCD_ERR_UNSUPPORTED, "outputs must be 16-byte aligned");
+  // everything the band calls check, before any HIP call
+  ttcd_status st = check_attn(a->q, a->k, a->v, a->o_t, a->B, a->Tk, a->Hq, a->Hkv, a->D, a->qs,
+                              a->ks, a->vs, a->os, a->dtype);
+  if (st == TTCD_OK) st = check_rescale(a->rescale_log2, a->dtype);
+  if (!(a->sm_scale > 0.f) || !isfinite(a->sm_scale))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "sm_scale must be finite and > 0");
+  if (st != TTCD_OK) return st;
   a->WT = window_t;
   a->WS = window_s;
   return TTCD_OK;
