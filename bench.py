@@ -178,8 +178,8 @@ def profile_one(args) -> int:
     'copy' is a plain device-to-device copy of 1 GiB (the known-size kernel used to
     calibrate the FETCH_SIZE / WRITE_SIZE counters)."""
     import torch
-    from oracle import attn_ref, conv_ref
     from ttcd_amd import causal_dwconv_x, fused_dual_window_attn, lse_dual_window_attn, window_attn
+    from ttcd_amd import work as W
 
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
@@ -194,17 +194,15 @@ def profile_one(args) -> int:
         norm = cfg["qk_norm"]
         fn = lambda: prologue.qk_norm_rope(q, k, w if norm else None, w if norm else None,  # noqa: E731
                                            1e-5, cos, sin)
-        from oracle import prologue_ref
-        work, unit = prologue_ref.prologue_bytes(B, T, H, HK, D), "GB/s"
+        work, unit = W.prologue_bytes(B, T, H, HK, D), "GB/s"
     elif args.only == "epilogue":
-        from oracle import epilogue_ref
         from ttcd_amd import epilogue
         Hd = cfg["hidden"]
         a_t, a_s, r = (torch.randn(B, T, Hd, device=dev, dtype=torch.bfloat16, generator=gen)
                        for _ in range(3))
         w = torch.ones(Hd, device=dev, dtype=torch.bfloat16)
         fn = lambda: epilogue.dual_residual_rmsnorm(a_t, a_s, r, w, cfg["norm_eps"])  # noqa: E731
-        work, unit = epilogue_ref.epilogue_bytes(B * T, Hd), "GB/s"
+        work, unit = W.epilogue_bytes(B * T, Hd), "GB/s"
     elif args.only == "copy":
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
@@ -212,12 +210,12 @@ def profile_one(args) -> int:
     elif args.only == "conv":
         x = torch.randn(1, 16, 4096, 3072, device=dev, dtype=torch.bfloat16, generator=gen)
         w = torch.randn(3072, 5, device=dev, dtype=torch.bfloat16, generator=gen)
-        fn, work, unit = (lambda: causal_dwconv_x(x, w)), conv_ref.conv_bytes(16, 4096, 3072, 5), "GB/s"
+        fn, work, unit = (lambda: causal_dwconv_x(x, w)), W.conv_bytes(16, 4096, 3072, 5), "GB/s"
     else:
         q = torch.randn(B, T, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
         k = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
         v = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
-        work, unit = attn_ref.attn_flops(B, H, D, T, wt), "TFLOP/s"
+        work, unit = W.attn_flops(B, H, D, T, wt), "TFLOP/s"
         if args.only == "fused":
             fn = lambda: fused_dual_window_attn(q, k, v, wt, ws, return_lse=True)  # noqa: E731
         elif args.only == "band":
@@ -236,8 +234,7 @@ def prologue_measure(q, k, cfg) -> dict:
     """The attention prologue (q/k RMSNorm + rotary, one pass) on the bench's own
     q and k: HBM-bound, so GB/s against the 8 TB/s peak."""
     import torch
-    from oracle import prologue_ref
-    from ttcd_amd import prologue
+    from ttcd_amd import prologue, work as W
 
     B, T, H, HK, D = q.shape[0], q.shape[1], q.shape[2], k.shape[2], q.shape[3]
     dev = q.device
@@ -248,7 +245,7 @@ def prologue_measure(q, k, cfg) -> dict:
     fn = lambda: prologue.qk_norm_rope(q, k, wq if norm else None, wq if norm else None,  # noqa: E731
                                        1e-5, cos, sin)
     ms_p = time_gpu(fn, 20, 3)
-    nbytes = prologue_ref.prologue_bytes(B, T, H, HK, D)
+    nbytes = W.prologue_bytes(B, T, H, HK, D)
     gbps = nbytes / (ms_p * 1e-3) / 1e9
     qk_bytes = B * T * (H + HK) * D * 2
     table_bytes = 2 * T * (D // 2) * 2
@@ -274,8 +271,7 @@ def sweep_measure(steps: int = 10, warmup: int = 2) -> list:
     LSE-combination variant at each sweep point; TFLOP/s over the teacher
     band F = 4*B*Hq*D*P(T, w_T) for both."""
     import torch
-    from oracle import attn_ref
-    from ttcd_amd import fused_dual_window_attn, lse_dual_window_attn
+    from ttcd_amd import fused_dual_window_attn, lse_dual_window_attn, work as W
 
     dev = torch.device("cuda:0")
     H, HK, D = 16, 8, 128
@@ -286,7 +282,7 @@ def sweep_measure(steps: int = 10, warmup: int = 2) -> list:
         q = torch.randn(B, T, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
         k = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
         v = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
-        F = attn_ref.attn_flops(B, H, D, T, wt)
+        F = W.attn_flops(B, H, D, T, wt)
         ms_f = time_gpu(lambda: fused_dual_window_attn(q, k, v, wt, ws, return_lse=True),
                         steps, warmup)
         ms_l = time_gpu(lambda: lse_dual_window_attn(q, k, v, wt, ws), steps, warmup)
@@ -346,8 +342,7 @@ def epilogue_measure(o_t, o_s, cfg) -> dict:
     the reference's two GEMMs (one per output) timed beside it."""
     import torch
     import torch.nn.functional as F
-    from oracle import epilogue_ref
-    from ttcd_amd import epilogue
+    from ttcd_amd import epilogue, work as W
 
     B, T = o_t.shape[0], o_t.shape[1]
     Hd, eps = cfg["hidden"], cfg["norm_eps"]
@@ -363,7 +358,7 @@ def epilogue_measure(o_t, o_s, cfg) -> dict:
     o_proj.weight.data.copy_(wo)
     norm = types.SimpleNamespace(weight=w, bias=None, eps=eps)
     ms_n = time_gpu(lambda: epilogue.dual_residual_rmsnorm(a_t, a_s, r, w, eps), 20, 3)
-    nbytes = epilogue_ref.epilogue_bytes(B * T, Hd)
+    nbytes = W.epilogue_bytes(B * T, Hd)
     gbps = nbytes / (ms_n * 1e-3) / 1e9
     ms_f = time_gpu(lambda: epilogue.fused_attn_epilogue(o_proj, norm, o_t, o_s, r), 20, 3)
     ot2, os2 = o_t.reshape(B, T, -1), o_s.reshape(B, T, -1)
@@ -377,6 +372,49 @@ def epilogue_measure(o_t, o_s, cfg) -> dict:
             "norm_ms": ms_n, "norm_GB_per_s": gbps, "norm_frac_of_hbm_peak": gbps / PEAK_HBM_GBPS,
             "norm_algorithmic_bytes": nbytes, "reference_norm_launches_bytes": ref_bytes,
             "drop_in_ms": ms_f, "stacked_gemm_ms": ms_g1, "two_gemms_ms": ms_g2}
+
+
+def second_shape_measure(name: str, steps: int = 10, warmup: int = 3) -> dict:
+    """The other BASELINE layer shape (config 3, SmolLM2-360M: Hq=15, Hkv=5,
+    D=64) timed like the headline: the fused kernel with both LSEs, the two
+    separate windowed calls, and the LSE variant; TFLOP/s over the teacher
+    band."""
+    import torch
+    from ttcd_amd import fused_dual_window_attn, lse_dual_window_attn, window_attn, work as W
+
+    cfg = CONFIGS[name]
+    B, T, H, HK, D, wt, ws = (cfg[k] for k in ("B", "T", "Hq", "Hkv", "D", "wt", "ws"))
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, T, H, D, device=dev, dtype=torch.bfloat16, generator=gen)
+    k = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
+    v = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
+    F, F_s = W.attn_flops(B, H, D, T, wt), W.attn_flops(B, H, D, T, ws)
+    ms = time_gpu(lambda: fused_dual_window_attn(q, k, v, wt, ws, return_lse=True), steps, warmup)
+    ms_two = time_gpu(lambda: (window_attn(q, k, v, wt), window_attn(q, k, v, ws)), steps, 2)
+    ms_lse = time_gpu(lambda: lse_dual_window_attn(q, k, v, wt, ws), steps, 2)
+    tf = F / (ms * 1e-3) / 1e12
+    log(f"{name}: fused {ms:.3f} ms {tf:.0f} TF/s ({100 * tf / PEAK_BF16_TFLOPS:.1f}%), "
+        f"two calls {ms_two:.3f} ms, LSE variant {ms_lse:.3f} ms")
+    return {"workload": cfg["name"], "B": B, "T": T, "Hq": H, "Hkv": HK, "head_dim": D,
+            "window_teacher": wt, "window_student": ws, "flops": F, "ms": ms, "tflops": tf,
+            "frac_of_bf16_peak": tf / PEAK_BF16_TFLOPS, "tokens_per_s": B * T / (ms * 1e-3),
+            "two_separate_calls_ms": ms_two, "fused_speedup_vs_two_calls": ms_two / ms,
+            "ideal_speedup_vs_two_calls": (F + F_s) / F, "lse_variant_ms": ms_lse}
+
+
+def source_hash(*names: str) -> str:
+    """sha256 over the named kernel sources (ttcd_amd/csrc), to tie a profile
+    measured on one build to the build being timed."""
+    import hashlib
+    h = hashlib.sha256()
+    for n in names:
+        with open(os.path.join(ROOT, "ttcd_amd", "csrc", n), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+ATTN_SOURCES = ("attn.hip", "schedule.h")
 
 
 def main() -> int:
@@ -401,9 +439,9 @@ def main() -> int:
         return 2
 
     import torch
-    from oracle import attn_ref, conv_ref
     from ttcd_amd import (causal_dwconv_x, fused_dual_window_attn, lse_dual_window_attn,
                           window_attn)
+    from ttcd_amd import work as W
 
     if args.only == "e2e":
         with torch.inference_mode():
@@ -429,8 +467,8 @@ def main() -> int:
     v = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
     torch.cuda.synchronize()
 
-    F = attn_ref.attn_flops(B, H, D, T, wt)
-    F_s = attn_ref.attn_flops(B, H, D, T, ws)
+    F = W.attn_flops(B, H, D, T, wt)
+    F_s = W.attn_flops(B, H, D, T, ws)
     res = {}
     with torch.inference_mode():
         fused = lambda: fused_dual_window_attn(q, k, v, wt, ws, return_lse=True)  # noqa: E731
@@ -468,7 +506,7 @@ def main() -> int:
             x = torch.randn(1, 16, 4096, 3072, device=dev, dtype=torch.bfloat16, generator=xg)
             w = torch.randn(3072, 5, device=dev, dtype=torch.bfloat16, generator=xg)
             ms_c = time_gpu(lambda: causal_dwconv_x(x, w), 20, 3)
-            nbytes = conv_ref.conv_bytes(16, 4096, 3072, 5)
+            nbytes = W.conv_bytes(16, 4096, 3072, 5)
             gbps = nbytes / (ms_c * 1e-3) / 1e9
             log(f"conv (1,16,4096,3072) K=5: {ms_c:.4f} ms, {gbps:.0f} GB/s")
             res["conv"] = {"shape": [1, 16, 4096, 3072], "K": 5, "ms": ms_c, "GB_per_s": gbps,
@@ -481,6 +519,8 @@ def main() -> int:
             res["epilogue"] = epilogue_measure(o_t, o_s, cfg)
             log(f"epilogue (o_proj + dual residual RMSNorm): {res['epilogue']}")
             del o_t, o_s
+            if args.config == "qwen3":
+                res["smollm2"] = second_shape_measure("smollm2")
             res["config4_sweep"] = sweep_measure()
             res["e2e_prefill"] = e2e_measure()
             # the length the reference's end-to-end numbers are quoted at
@@ -490,15 +530,19 @@ def main() -> int:
                 "hardware": "one H100 80GB", "source": "profiling/REPORT.md:25, :321",
                 "note": "other hardware and the reference's generate() prefill; context only"}
             res["e2e_prefill_64k"] = e64
-    if not args.no_numerics:
-        res["numerics_config1"] = numerics_report()
-        log(f"numerics: {res['numerics_config1']}")
-
-    traffic = None
+    # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE / WRITE_SIZE) on
+    # the build whose attention sources hash to `attn_sources_sha256`; dropped
+    # (null) when the sources timed here differ
+    traffic, traffic_note = None, "no HBM-traffic profile for this config"
     tpath = os.path.join(ROOT, "profiles", f"hbm_traffic_{args.config}.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("fused_dual_window_attn_bytes_per_launch")
+            tj = json.load(f)
+        if tj.get("attn_sources_sha256") == source_hash(*ATTN_SOURCES):
+            traffic = tj.get("fused_dual_window_attn_bytes_per_launch")
+            traffic_note = f"rocprofv3 FETCH_SIZE/WRITE_SIZE, {os.path.basename(tpath)}"
+        else:
+            traffic_note = "stale: profile measured on other attention sources"
 
     out = {
         "metric": METRIC,
@@ -520,14 +564,21 @@ def main() -> int:
         "tokens_per_s": B * T / (ms * 1e-3),
         "flops_per_step": F,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": traffic},
+                     "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": traffic,
+                     "traffic_source": traffic_note},
         **res,
     }
+    # The CPU leg: the reference's CPU path (restated in oracle/), timed as the
+    # cpu_baseline and used as the checker of the config-1 numerics. No other
+    # part of this file touches oracle/.
     if not args.no_cpu:
         log("CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline(q, k, v, cfg, args.cpu_seconds)
         log(f"cpu_baseline: {out['cpu_baseline']['value']:.4f} TFLOP/s "
             f"on {out['cpu_baseline']['cores']} threads")
+        if not args.no_numerics:
+            out["numerics_config1"] = numerics_report()
+            log(f"numerics: {out['numerics_config1']}")
     print(json.dumps(out), flush=True)
     return 0
 

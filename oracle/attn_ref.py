@@ -5,9 +5,6 @@ this module, as the checker. Everything runs in torch on the CPU in fp32 (or
 fp64 where stated); nothing here touches the GPU.
 
 Functions and the reference lines they restate
-  band_pairs / attn_flops       - the algorithmic work count: pairs (i, j),
-                                  0 <= j <= i < T with lo <= i - j < hi; FLOPs =
-                                  4 * B * H * D * pairs (QK^T + PV).
   dense_reference               - test/test_fused_dual_attn.py:88-110 (fp32
                                   einsum, repeat_interleave GQA, bottom-right
                                   alignment, mask 0 <= i - j < W, softmax), with
@@ -42,26 +39,6 @@ NEG_INF = float("-inf")
 
 
 # --------------------------------------------------------------------------- counts
-def band_pairs(T: int, lo: int, hi: int) -> int:
-    """#(i, j) with 0 <= j <= i < T and lo <= i - j < hi."""
-    hi = min(hi, T)
-    if hi <= lo:
-        return 0
-    n = hi - lo
-    return n * T - (lo + hi - 1) * n // 2
-
-
-def window_pairs(T: int, W: int | None) -> int:
-    """P(T, W) = W(W+1)/2 + (T-W)W for W <= T, else T(T+1)/2."""
-    if W is None or W < 0 or W >= T:
-        return T * (T + 1) // 2
-    return W * (W + 1) // 2 + (T - W) * W
-
-
-def attn_flops(B: int, H: int, D: int, T: int, W: int | None) -> int:
-    return 4 * B * H * D * window_pairs(T, W)
-
-
 # --------------------------------------------------------------------------- references
 def _norm_window(W, T):
     return T if (W is None or W < 0) else W

@@ -109,8 +109,3 @@ def conv1d_reference(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     xf = F.pad(xf, (K - 1, 0))
     y = F.conv1d(xf, w.detach().cpu().double().view(D, 1, K), groups=D)
     return y.transpose(1, 2).reshape(*lead, C, D)
-
-
-def conv_bytes(N: int, C: int, D: int, K: int, elem: int = 2, w_elem: int = 2) -> int:
-    """Algorithmic HBM bytes of one call: read x once, write y once, read w."""
-    return 2 * N * C * D * elem + D * K * w_elem

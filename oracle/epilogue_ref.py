@@ -1,7 +1,7 @@
 """CPU oracle for the attention epilogue (TEST INFRASTRUCTURE ONLY).
 
-Only tests/, __graft_entry__.smoke() and bench.py may use this module, as
-the checker.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
+this module, as the checker.
 
   residual_rms_norm_ref  fla's RMSNorm forward with a residual and prenorm
                          (fla/modules/layernorm.py:189-251 with HAS_RESIDUAL,
@@ -13,7 +13,6 @@ the checker.
   dual_residual_rms_norm_ref
                          the teacher and the student call of
                          profiling/patches.py:296-298 on one residual.
-  epilogue_bytes         algorithmic HBM bytes of the fused launch.
 
 Pins (tests/test_epilogue.py): residual_out == the float64 sum rounded to the
 dtype; y within one rounding of a float64 evaluation; a = -residual gives
@@ -47,9 +46,3 @@ def dual_residual_rms_norm_ref(a_t, a_s, residual, w, eps):
     y_t, res_out = residual_rms_norm_ref(a_t, residual, w, eps)
     y_s, _ = residual_rms_norm_ref(a_s, residual, w, eps)
     return y_t, res_out, y_s
-
-
-def epilogue_bytes(rows: int, hidden: int, elem: int = 2, w_elem: int = 2) -> int:
-    """Three (rows, hidden) reads (attn_t, attn_s, residual), three writes
-    (hidden_states, residual_out, student_output), the weight once."""
-    return 6 * rows * hidden * elem + hidden * w_elem

@@ -1,6 +1,6 @@
 """CPU oracle for the attention prologue (TEST INFRASTRUCTURE ONLY).
 
-Only tests/, __graft_entry__.smoke() and bench.py may use this module, as
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use this module, as
 the checker.
 
   inv_freq_ref        fp32 1 / base ** (arange(0, dim, 2) / dim)
@@ -97,9 +97,3 @@ def qk_norm_rope_ref(q, k, q_w, k_w, eps, cos, sin, seqlen_offset=0):
     if q_w is not None:
         q, k = rms_norm_ref(q, q_w, eps), rms_norm_ref(k, k_w, eps)
     return rope_ref(q, cos, sin, seqlen_offset), rope_ref(k, cos, sin, seqlen_offset)
-
-
-def prologue_bytes(B: int, T: int, Hq: int, Hkv: int, D: int, elem: int = 2) -> int:
-    """Algorithmic HBM bytes of one fused launch: q and k read once and written
-    once (the cos/sin rows, T x D elements, are shared by every head)."""
-    return 2 * B * T * (Hq + Hkv) * D * elem + 2 * T * (D // 2) * elem

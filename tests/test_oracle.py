@@ -18,6 +18,7 @@ import pytest
 import torch
 
 from oracle import attn_ref, conv_ref
+from ttcd_amd import work
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -28,6 +29,7 @@ def _qkv(T, H, HK, D, seed, dtype=torch.bfloat16, B=1):
 
 
 # ----------------------------------------------------------------------------- counts
+# the product's work counts (ttcd_amd/work.py), pinned by brute force
 def test_band_pair_counts_brute_force():
     for T in (1, 7, 64, 129):
         i = np.arange(T)[:, None]
@@ -35,18 +37,18 @@ def test_band_pair_counts_brute_force():
         d = i - j
         for lo, hi in ((0, 1), (0, 5), (3, 9), (0, T), (0, 10 * T), (2, T + 5)):
             want = int(((d >= lo) & (d < hi)).sum())
-            assert attn_ref.band_pairs(T, lo, hi) == want
+            assert work.band_pairs(T, lo, hi) == want
             if lo == 0:
-                assert attn_ref.window_pairs(T, hi) == want
+                assert work.window_pairs(T, hi) == want
 
 
 def test_headline_flop_constants():
     # Headline figures: P(65536, 8192) = 8192*8193/2 + (65536-8192)*8192 pairs per head,
     # and the teacher / student band FLOPs (4*D per pair, B=1, Hq=16, D=128).
-    assert attn_ref.window_pairs(65536, 8192) == 503_320_576
-    assert attn_ref.window_pairs(2048, 512) == 917_760
-    assert abs(attn_ref.attn_flops(1, 16, 128, 65536, 8192) - 4.1232e12) < 1e8
-    assert abs(attn_ref.attn_flops(1, 16, 128, 65536, 4096) - 2.1303e12) < 1e8
+    assert work.window_pairs(65536, 8192) == 503_320_576
+    assert work.window_pairs(2048, 512) == 917_760
+    assert abs(work.attn_flops(1, 16, 128, 65536, 8192) - 4.1232e12) < 1e8
+    assert abs(work.attn_flops(1, 16, 128, 65536, 4096) - 2.1303e12) < 1e8
 
 
 # ----------------------------------------------------------------------------- attention

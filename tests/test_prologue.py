@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import attn_ref, prologue_ref
-from ttcd_amd import _lib, prologue
+from ttcd_amd import _lib, prologue, work
 
 
 def _rand(shape, dtype=torch.bfloat16, seed=0, scale=1.0):
@@ -116,7 +116,7 @@ def test_tables_and_inv_freq_closed_forms():
 
 def test_prologue_bytes():
     # q and k read and written once + the table rows
-    assert prologue_ref.prologue_bytes(1, 65536, 16, 8, 128) == (
+    assert work.prologue_bytes(1, 65536, 16, 8, 128) == (
         2 * 65536 * 24 * 128 * 2 + 2 * 65536 * 64 * 2)
 
 

@@ -684,12 +684,16 @@ void attn_fwd_kernel(AttnArgs a) {
       const float m_new = active ? fmaxf(m, mx) : m;
       const bool grow = (m_new > m) & ((m == -INFINITY) | ((m_new - m) * x.c > rescale_log2));
       if (__builtin_expect(__any(grow) != 0, 0)) {
-        const float mc_new = (m_new == -INFINITY) ? 0.f : m_new * x.c;
-        const float alpha = fast_exp2(fmaf(m, x.c, -mc_new));
+        // Only the lanes past the threshold move their reference max (the
+        // others keep theirs, alpha = 1), so every row's arithmetic depends
+        // on its own scores alone, not on the other rows of its wavefront.
+        const float m_set = grow ? m_new : m;
+        const float mc_new = (m_set == -INFINITY) ? 0.f : m_set * x.c;
+        const float alpha = grow ? fast_exp2(fmaf(m, x.c, -mc_new)) : 1.f;
         l *= alpha;
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) o[dt] *= alpha;
-        m = m_new;
+        m = m_set;
       }
       return active ? ((m == -INFINITY) ? 0.f : m * x.c) : INFINITY;
     };
