@@ -207,6 +207,31 @@ ttcd_status ttcd_lse_dual_window_attn_fwd(
     ttcd_dtype dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Allocation-free form of ttcd_lse_dual_window_attn_fwd. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The workspace is a fixed device array inside the library,
+ * ttcd_lse_dual_window_attn_noalloc_scratch_bytes() (64 MiB) per GPU, held
+ * until the process ends; the call makes no allocation of its own. Rows run
+ * in chunks that fit it, so any T works; TTCD_ERR_UNSUPPORTED when a single
+ * query row does not fit (B * Hq * (2 * D + 8) bytes, i.e. B * Hq above
+ * ~254,000 at D = 128). Results are bit-identical to
+ * ttcd_lse_dual_window_attn_fwd. Every call on one GPU shares the array:
+ * calls that overlap in time on one GPU (different streams with no ordering
+ * between them) race; calls on one stream are safe. The first call on a
+ * device resolves the array's address there (hipGetSymbolAddress). Other
+ * arguments as in ttcd_lse_dual_window_attn_fwd.
+ */
+size_t ttcd_lse_dual_window_attn_noalloc_scratch_bytes(void);
+ttcd_status ttcd_lse_dual_window_attn_noalloc_fwd(
+    const void* q, const void* k, const void* v, void* o_t, void* o_s,
+    int B, int Tq, int Tk, int Hq, int Hkv, int D,
+    const int64_t q_stride[4], const int64_t k_stride[4],
+    const int64_t v_stride[4], const int64_t o_stride[4],
+    int window_t, int window_s, float sm_scale, float rescale_log2,
+    ttcd_dtype dtype, void* stream);
+
+/*
  * Chunk-local causal depthwise conv along C on the (N, C, D) layout.
  * Replaces causal_dwconv_chunked / _causal_dwconv_fwd
  * (profiling/fused_conv.py:24-61) and IPTTCDMLP._apply_ttt_conv with

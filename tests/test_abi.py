@@ -182,3 +182,26 @@ def test_f16_rescale_threshold_bounded_by_f16_range(rescale):
         _lib.DTYPE_F16, None) == _lib.TTCD_ERR_INVALID_ARGUMENT
     assert _varlen_call("dual", dtype=_lib.DTYPE_F16, rescale=rescale) == \
         _lib.TTCD_ERR_INVALID_ARGUMENT
+
+
+def test_noalloc_lse_variant_rejects_rows_beyond_its_scratch():
+    """The allocation-free LSE variant refuses, before any HIP call, a shape
+    whose single query row does not fit its fixed scratch."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x10000)
+    cap = lib.ttcd_lse_dual_window_attn_noalloc_scratch_bytes()
+    assert cap == 64 << 20
+    Hq = cap // (2 * 128 + 8) + 8            # one row of B * Hq * (2D + 8) bytes > cap
+    qs = _lib.strides4([64 * Hq * 128, Hq * 128, 128, 1])
+    ks = _lib.strides4([64 * 128, 128, 128, 1])
+    st = lib.ttcd_lse_dual_window_attn_noalloc_fwd(
+        p, p, p, p, p, 1, 64, 64, Hq, 1, 128, qs, ks, ks, qs, 32, 16, 128 ** -0.5, 8.0,
+        _lib.DTYPE_BF16, None)
+    assert st == _lib.TTCD_ERR_UNSUPPORTED
+    assert b"scratch" in lib.ttcd_last_error()
+    # the reference's strict gap (lse_dual_attn.py:20) holds here too
+    assert lib.ttcd_lse_dual_window_attn_noalloc_fwd(
+        p, p, p, p, p, 1, 64, 64, 4, 2, 64, _lib.strides4([64 * 256, 256, 64, 1]),
+        _lib.strides4([64 * 128, 128, 64, 1]), _lib.strides4([64 * 128, 128, 64, 1]),
+        _lib.strides4([64 * 256, 256, 64, 1]), 16, 16, 0.125, 8.0, _lib.DTYPE_BF16,
+        None) == _lib.TTCD_ERR_INVALID_ARGUMENT

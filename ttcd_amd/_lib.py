@@ -38,6 +38,8 @@ EXPORTS = (
     "ttcd_lse_merge_fwd",
     "ttcd_lse_dual_window_attn_workspace_bytes",
     "ttcd_lse_dual_window_attn_fwd",
+    "ttcd_lse_dual_window_attn_noalloc_scratch_bytes",
+    "ttcd_lse_dual_window_attn_noalloc_fwd",
     "ttcd_causal_dwconv_chunked_fwd",
     "ttcd_qk_norm_rope_fwd",
     "ttcd_rope_table_fwd",
@@ -100,6 +102,12 @@ _SIGS = {
         _i32, _i32, _i32, _i32, _i32, _i32,
         _i64x4, _i64x4, _i64x4, _i64x4,
         _i32, _i32, ctypes.c_float, ctypes.c_float, _i32, _vp, ctypes.c_size_t, _vp]),
+    "ttcd_lse_dual_window_attn_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "ttcd_lse_dual_window_attn_noalloc_fwd": (_i32, [
+        _vp, _vp, _vp, _vp, _vp,
+        _i32, _i32, _i32, _i32, _i32, _i32,
+        _i64x4, _i64x4, _i64x4, _i64x4,
+        _i32, _i32, ctypes.c_float, ctypes.c_float, _i32, _vp]),
     "ttcd_causal_dwconv_chunked_fwd": (_i32, [
         _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp]),
     "ttcd_qk_norm_rope_fwd": (_i32, [

@@ -8,6 +8,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "internal.h"
 #include "schedule.h"
 #include "ttcd.h"
@@ -513,6 +515,84 @@ ttcd_status ttcd_lse_dual_window_attn_fwd(const void* q, const void* k, const vo
   if (workspace_bytes > 0 && (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u)))
     return fail(TTCD_ERR_INVALID_ARGUMENT, "workspace must be non-null and 256-byte aligned");
   return run_lse_dual(a, static_cast<char*>(workspace), workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free LSE variant. Its scratch is a file-scope device array: one
+// copy per GPU the library runs on, held until the process ends. On the host
+// the array's name is only a stand-in, never a device address: the address
+// is resolved once per device with hipGetSymbolAddress (that device current)
+// and only that pointer is passed to kernels. Every call on one GPU shares the
+// array; the variant writes each scratch element before reading it, so
+// nothing needs clearing, but calls that overlap in time on one GPU (different
+// streams without ordering) race on it.
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+}  // namespace
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device of `stream` (the current device
+// for the null stream), resolved on first use there.
+ttcd_status scratch_for(void* stream, char** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return from_hip(e, "hipGetDevice");
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t d = 0;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &d);
+    if (e != hipSuccess) return from_hip(e, "hipStreamGetDevice");
+    dev = d;
+  }
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(TTCD_ERR_UNSUPPORTED, "device %d beyond the %d the scratch table holds", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur) {
+      e = hipSetDevice(dev);
+      if (e != hipSuccess) return from_hip(e, "hipSetDevice");
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess && e2 != hipSuccess) e = e2;
+    }
+    if (e != hipSuccess) return from_hip(e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr || (reinterpret_cast<uintptr_t>(p) & 255u) != 0)
+      return fail(TTCD_ERR_HIP, "scratch symbol has no 256-byte aligned device address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = static_cast<char*>(g_scratch_ptr[dev]);
+  return TTCD_OK;
+}
+}  // namespace
+
+size_t ttcd_lse_dual_window_attn_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+ttcd_status ttcd_lse_dual_window_attn_noalloc_fwd(
+    const void* q, const void* k, const void* v, void* o_t, void* o_s, int B, int Tq, int Tk,
+    int Hq, int Hkv, int D, const int64_t q_stride[4], const int64_t k_stride[4],
+    const int64_t v_stride[4], const int64_t o_stride[4], int window_t, int window_s,
+    float sm_scale, float rescale_log2, ttcd_dtype dtype, void* stream) {
+  LseDual a = {q, k, v, o_t, o_s, B, Tq, Tk, Hq, Hkv, D, 0, 0, q_stride, k_stride, v_stride,
+               o_stride, sm_scale, rescale_log2, dtype};
+  ttcd_status st = check_lse_dual(&a, window_t, window_s);
+  if (st != TTCD_OK) return st;
+  if (a.n0() < a.Tq && a.rows_fitting(kNoAllocScratchBytes) < 1)
+    return fail(TTCD_ERR_UNSUPPORTED,
+                "B * Hq too large for the %zu-byte scratch: one query row needs %zu bytes",
+                kNoAllocScratchBytes, a.chunk_bytes(1));
+  char* ws = nullptr;
+  st = scratch_for(stream, &ws);
+  if (st != TTCD_OK) return st;
+  return run_lse_dual(a, ws, kNoAllocScratchBytes, stream);
 }
 
 ttcd_status ttcd_causal_dwconv_chunked_fwd(const void* x, const void* w, void* y, int64_t N,
