@@ -372,6 +372,35 @@ ttcd_status ttcd_ttt_features_fwd(const void* gu_t, const void* gu_s,
                                   int inter, ttcd_dtype dtype, void* stream);
 
 /*
+ * The TTT MLP's update scan around its GEMMs (the group loop of
+ * custom_models/ipttcd/modeling_ipttcdv9_lowcopy_scanfuse.py:121-172).
+ *
+ * ttcd_ttt_proj_beta_t_fwd: pdt[b*nupd + c, h, t] = pd[(b*nupd + c)*chunk + t, h]
+ * * beta[b*beta_batch_stride + c*chunk + t], one rounding to dtype (the
+ * dynamic learning rate, :126-127; beta NULL: no scaling), written transposed
+ * per chunk, (B*nupd, H, chunk) contiguous, so that dW_c = pd_c^T z_hat_c
+ * (:146-149) is one batched GEMM on contiguous operands. pd rows have stride
+ * pd_stride elements.
+ *
+ * ttcd_ttt_scan_fwd: one update group. dw (nupd, H, inter) the group's chunk
+ * updates, w_cur (H, inter) the weight at the group start. With acc_j the
+ * running sum of dw[0..j] stored in dtype after every step (torch's GPU scan
+ * of a bf16 tensor, :157) and cs_j = lr * acc_j rounded (:157), writes
+ * steps_t[0] = w_cur^T and steps_t[s] = (w_cur + cs_{s-1})^T rounded for
+ * s = 1 .. nsteps-1 (the chunk weights of :161-165), (nsteps, inter, H)
+ * contiguous; and, if w_next is not NULL, w_next = w_cur + cs_{nupd-1}
+ * rounded (:169-170). Requires nsteps <= nupd + 1. lr is the learning rate
+ * as the dtype stores it. All additions and products in fp32, each rounded
+ * once to dtype, as torch's bf16 ops round them.
+ */
+ttcd_status ttcd_ttt_proj_beta_t_fwd(const void* pd, int64_t pd_stride, const void* beta,
+                                    int64_t beta_batch_stride, void* pdt, int B, int nupd,
+                                    int chunk, int H, ttcd_dtype dtype, void* stream);
+ttcd_status ttcd_ttt_scan_fwd(const void* dw, const void* w_cur, float lr, void* steps_t,
+                              void* w_next, int nupd, int nsteps, int H, int inter,
+                              ttcd_dtype dtype, void* stream);
+
+/*
  * Host-only schedule check (no GPU work). Replays the attention kernels'
  * exact tile/phase schedule for one (b, h) slice of length T and adds, for
  * every (query i, key j) pair the kernel would fold into each output, one

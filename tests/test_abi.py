@@ -205,3 +205,19 @@ def test_noalloc_lse_variant_rejects_rows_beyond_its_scratch():
         _lib.strides4([64 * 128, 128, 64, 1]), _lib.strides4([64 * 128, 128, 64, 1]),
         _lib.strides4([64 * 256, 256, 64, 1]), 16, 16, 0.125, 8.0, _lib.DTYPE_BF16,
         None) == _lib.TTCD_ERR_INVALID_ARGUMENT
+
+
+def test_ttt_scan_entry_points_reject_bad_arguments():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(0x10000)
+    # ttcd_ttt_proj_beta_t_fwd(pd, pd_stride, beta, beta_bs, pdt, B, nupd, chunk, H, dtype, stream)
+    assert lib.ttcd_ttt_proj_beta_t_fwd(None, 64, p, 256, p, 1, 2, 128, 64, 0, None) == 1
+    assert lib.ttcd_ttt_proj_beta_t_fwd(p, 32, p, 256, p, 1, 2, 128, 64, 0, None) == 1  # stride < H
+    assert lib.ttcd_ttt_proj_beta_t_fwd(p, 64, p, 100, p, 1, 2, 128, 64, 0, None) == 1  # beta stride
+    assert lib.ttcd_ttt_proj_beta_t_fwd(p, 64, p, 256, p, 1, 2, 128, 64, 2, None) == 2  # f32
+    # ttcd_ttt_scan_fwd(dw, w_cur, lr, steps_t, w_next, nupd, nsteps, H, inter, dtype, stream)
+    assert lib.ttcd_ttt_scan_fwd(p, p, 0.3, p, None, 2, 4, 64, 64, 0, None) == 1  # nsteps > nupd+1
+    assert lib.ttcd_ttt_scan_fwd(None, p, 0.3, p, None, 2, 2, 64, 64, 0, None) == 1
+    assert lib.ttcd_ttt_scan_fwd(p, p, 0.3, p, p, 0, 1, 64, 64, 0, None) == 1     # w_next, no update
+    assert lib.ttcd_ttt_scan_fwd(p, p, float("nan"), p, None, 2, 2, 64, 64, 0, None) == 1
+    assert lib.ttcd_ttt_scan_fwd(p, p, 0.3, p, None, 2, 2, 64, 64, 2, None) == 2

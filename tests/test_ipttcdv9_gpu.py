@@ -125,6 +125,7 @@ def test_ttt_mlp_matches_oracle_loop(B, L, C, G):
     with torch.inference_mode():
         y = ttt.ttt_mlp(x, t, w, chunk=C, lr=0.3, update_every=G)
         y2 = ttt.ttt_mlp(x, t, w, chunk=C, lr=0.3, update_every=G, fused=False)
+        y3 = ttt.ttt_mlp(x, t, w, chunk=C, lr=0.3, update_every=G, scan="torch")
         # the oracle loop on the kernel's own features (same padding as the model)
         nch = -(-L // C)
         pad = nch * C - L
@@ -137,6 +138,9 @@ def test_ttt_mlp_matches_oracle_loop(B, L, C, G):
     torch.cuda.synchronize()
     # fused and separate feature passes are the same values, so the same output
     assert torch.equal(y, y2)
+    # the scan kernels + batched GEMMs vs the reference's per-chunk torch ops:
+    # the same roundings, the GEMMs' accumulation order may differ
+    _logits_close(y, y3, max_frac=2e-2, mean_frac=1e-2)
     cpu = lambda v: v.cpu()  # noqa: E731
     want = R.ttt_mlp_scan_ref(cpu(z), cpu(zh), cpu(diff), cpu(tp), cpu(w.down), cpu(w.ttt_proj),
                               cpu(w.b_proj), lr=0.3, update_every=G, B=B, nchunk=nch, C=C)[:, :L]
@@ -147,6 +151,54 @@ def test_ttt_mlp_matches_oracle_loop(B, L, C, G):
     assert (yf - wf).abs().max() <= 3e-2 * wf.abs().max()
     if nch > 1:  # the update path is exercised: the output is not the plain MLP's
         assert (wf - plain).norm() / wf.norm() > 0.05
+
+
+@pytest.mark.parametrize("B,K,C,H,dt,with_beta", [
+    (1, 7, 256, 256, torch.bfloat16, True), (2, 3, 100, 72, torch.bfloat16, True),
+    (1, 2, 64, 130, torch.float16, False)])
+def test_proj_beta_t_is_torchs_multiply_transposed(B, K, C, H, dt, with_beta):
+    """pd * beta (one rounding, the reference's bf16 multiply) written per chunk
+    transposed, bit for bit against torch's own GPU ops."""
+    pd = _rand(B * K * C, H, seed=K, scale=3.0, dtype=dt).to(DEV)
+    beta = torch.sigmoid(_rand(B, K + 1, C, seed=C, dtype=torch.float32)).to(dt).to(DEV)
+    with torch.inference_mode():
+        got = ttt.proj_beta_t(pd, beta if with_beta else None, B, K, C)
+        want = pd.view(B, K, C, H)
+        if with_beta:
+            want = want * beta[:, :K, :, None]
+        want = want.transpose(-1, -2).reshape(B * K, H, C)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("nupd,nsteps,H,I,dt", [
+    (7, 8, 256, 384, torch.bfloat16), (16, 16, 128, 256, torch.bfloat16),
+    (3, 3, 100, 72, torch.bfloat16), (5, 6, 64, 200, torch.float16), (0, 1, 96, 64, torch.bfloat16)])
+def test_scan_steps_are_torchs_bf16_scan(nupd, nsteps, H, I, dt):
+    """The update scan of one group (scanfuse.py:157-170) against torch's own
+    GPU ops, bit for bit: cumsum (a running sum stored in the dtype after
+    every step), lr * cumsum, W_cur + cs for every chunk, the next W_cur; and
+    torch's GPU cumsum against the oracle's step-wise scan."""
+    dw = _rand(max(nupd, 1), H, I, seed=nupd + H, scale=2.0, dtype=dt)[:nupd].contiguous()
+    w0 = _rand(H, I, seed=7, scale=0.05, dtype=dt)
+    lr = 0.3
+    with torch.inference_mode():
+        steps, w_next = ttt.scan_steps(dw.to(DEV) if nupd else None, w0.to(DEV), lr, nsteps,
+                                       want_next=nupd > 0)
+        wc = w0.to(DEV)
+        want = [wc]
+        if nupd:
+            csum = torch.cumsum(dw.to(DEV), dim=0)
+            cs = torch.tensor(lr, dtype=dt, device=DEV) * csum
+            want += [wc + cs[j] for j in range(nsteps - 1)]
+            want_next = wc + cs[-1]
+    torch.cuda.synchronize()
+    assert steps.shape == (nsteps, I, H)
+    for s_ in range(nsteps):
+        assert torch.equal(steps[s_], want[s_].t()), s_
+    if nupd:
+        assert torch.equal(w_next, want_next)
+        assert torch.equal(csum.cpu(), R.cumsum_stepwise(dw, 0))
 
 
 # -------------------------------------------------------------------- model

@@ -48,6 +48,8 @@ EXPORTS = (
     "ttcd_add_rmsnorm_fwd",
     "ttcd_swiglu_fwd",
     "ttcd_ttt_features_fwd",
+    "ttcd_ttt_proj_beta_t_fwd",
+    "ttcd_ttt_scan_fwd",
     "ttcd_attn_schedule_coverage",
 )
 
@@ -125,6 +127,10 @@ _SIGS = {
     "ttcd_ttt_features_fwd": (_i32, [
         _vp, _vp, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp,
         _i32, _i32, _i32, _i32, _i32, _vp]),
+    "ttcd_ttt_proj_beta_t_fwd": (_i32, [
+        _vp, _i64, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "ttcd_ttt_scan_fwd": (_i32, [
+        _vp, _vp, ctypes.c_float, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp]),
     "ttcd_attn_schedule_coverage": (_i32, [
         _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
 }

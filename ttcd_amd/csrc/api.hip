@@ -840,6 +840,45 @@ ttcd_status ttcd_ttt_features_fwd(const void* gu_t, const void* gu_s, int64_t gu
                   "ttt features launch");
 }
 
+ttcd_status ttcd_ttt_proj_beta_t_fwd(const void* pd, int64_t pd_stride, const void* beta,
+                                    int64_t beta_batch_stride, void* pdt, int B, int nupd,
+                                    int chunk, int H, ttcd_dtype dtype, void* stream) {
+  if (!pd || !pdt) return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (B < 1 || nupd < 1 || chunk < 1 || H < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need B, nupd, chunk, H >= 1");
+  if (pd_stride < H || (beta && beta_batch_stride < (int64_t)nupd * chunk))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "pd row stride must be >= H and the beta batch "
+                                           "stride >= nupd * chunk");
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "dtype must be bf16 or f16");
+  if ((int64_t)B * nupd > 65535)
+    return fail(TTCD_ERR_UNSUPPORTED, "B * nupd above 65535 (grid z)");
+  ttcd::TttProjBetaArgs a{pd, pd_stride, beta, beta_batch_stride, pdt, B, nupd, chunk, H};
+  return from_hip(ttcd::launch_ttt_proj_beta_t(a, elem(dtype), static_cast<hipStream_t>(stream)),
+                  "ttt pd*beta launch");
+}
+
+ttcd_status ttcd_ttt_scan_fwd(const void* dw, const void* w_cur, float lr, void* steps_t,
+                              void* w_next, int nupd, int nsteps, int H, int inter,
+                              ttcd_dtype dtype, void* stream) {
+  if (!w_cur || !steps_t || (nupd > 0 && !dw))
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (H < 1 || inter < 1 || nupd < 0 || nsteps < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "need H, inter, nsteps >= 1 and nupd >= 0");
+  // chunk s of the group uses cs[s - 1]: there must be one for every step but the first
+  if (nsteps > nupd + 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "nsteps (%d) must be <= nupd + 1 (%d)", nsteps,
+                nupd + 1);
+  if (w_next && nupd < 1)
+    return fail(TTCD_ERR_INVALID_ARGUMENT, "w_next needs at least one update");
+  if (!isfinite(lr)) return fail(TTCD_ERR_INVALID_ARGUMENT, "lr must be finite");
+  if (dtype != TTCD_DTYPE_BF16 && dtype != TTCD_DTYPE_F16)
+    return fail(TTCD_ERR_UNSUPPORTED, "dtype must be bf16 or f16");
+  ttcd::TttScanArgs a{dw, w_cur, lr, steps_t, w_next, nupd, nsteps, H, inter};
+  return from_hip(ttcd::launch_ttt_scan(a, elem(dtype), static_cast<hipStream_t>(stream)),
+                  "ttt scan launch");
+}
+
 ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int window_t,
                                         int gqa_group, int32_t* counts_near,
                                         int32_t* counts_far) {

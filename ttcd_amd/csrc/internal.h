@@ -102,6 +102,26 @@ hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t ro
 hipError_t launch_ttt_features(const TttFeatureArgs& a, Elem dtype, Elem w_dtype,
                                hipStream_t stream);
 
+// The TTT update scan (ttt.hip).
+struct TttProjBetaArgs {
+  const void* pd;      // (B * nupd * C, H) rows, row stride pd_stride
+  int64_t pd_stride;
+  const void* beta;    // per token: b * beta_sb + c * C + t, or null (no scaling)
+  int64_t beta_sb;
+  void* pdt;           // (B * nupd, H, C) contiguous
+  int B, nupd, C, H;
+};
+struct TttScanArgs {
+  const void* dw;      // (nupd, H, I) contiguous
+  const void* w_cur;   // (H, I) contiguous
+  float lr;            // the learning rate as stored in the dtype
+  void* steps_t;       // (nsteps, I, H) contiguous: W_step transposed
+  void* w_next;        // (H, I) or null: W_cur + cs[nupd - 1]
+  int nupd, nsteps, H, I;
+};
+hipError_t launch_ttt_proj_beta_t(const TttProjBetaArgs& a, Elem dtype, hipStream_t stream);
+hipError_t launch_ttt_scan(const TttScanArgs& a, Elem dtype, hipStream_t stream);
+
 hipError_t launch_dwconv(const void* x, const void* w, void* y, int64_t N, int C,
                          int D, int K, Elem xt, Elem wt, hipStream_t stream);
 

@@ -29,6 +29,19 @@
 // and keeps the K-1 previous rows of both feature streams in registers, as
 // the standalone conv kernel does. The halo rows at the start of a run are
 // recomputed from gate / up (L2 hits: the neighbouring run streams them).
+//
+// The update scan of the group loop (scanfuse.py:121-172) around its GEMMs:
+// ttt_pd_beta_t_kernel writes pd * beta (the projected difference scaled by
+// the per-token learning rate, :126-127, one bf16 multiply) transposed per
+// chunk, (chunk, H, C), so the update GEMM dW_c = pd_c^T z_hat_c (:146-149)
+// runs as one batched GEMM on contiguous operands; ttt_scan_kernel then does
+// what the reference does in three torch launches per group plus one add per
+// chunk (:157-170): the running sum over the group's chunk updates with the
+// sum stored in the dtype after every step (torch's GPU scan of a bf16
+// tensor), cs_j = lr * sum_j rounded, W_step = W_cur + cs rounded, and the
+// next group's W_cur; it writes every chunk's W_step transposed, (step, I, H),
+// so the per-chunk output GEMMs z_c W_step^T (:161-165) are one batched GEMM
+// on contiguous operands as well. Both transpose through 64 x 64 LDS tiles.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -234,6 +247,112 @@ hipError_t launch_sw(const void* g, const void* u, void* o, int64_t rows, int co
   return hipGetLastError();
 }
 
+// 64 x 64 tile transposes for the update scan. Thread (tx, ty) = (tid % 64,
+// tid / 64) handles rows ty, ty + 4, ... of a tile; the LDS tile is fp32 with
+// a 65-word row pitch, so the transposed reads are free of bank conflicts.
+constexpr int kTile = 64;
+
+template <typename T>
+__global__ __launch_bounds__(256) void ttt_pd_beta_t_kernel(TttProjBetaArgs a) {
+  __shared__ float tile[kTile][kTile + 1];
+  const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;
+  const int h0 = blockIdx.x * kTile, t0 = blockIdx.y * kTile, bk = blockIdx.z;
+  const int b = bk / a.nupd, c = bk % a.nupd;
+  const T* pd = static_cast<const T*>(a.pd) + (int64_t)bk * a.C * a.pd_stride;
+  const T* beta = a.beta ? static_cast<const T*>(a.beta) + b * a.beta_sb + (int64_t)c * a.C
+                         : nullptr;
+#pragma unroll
+  for (int r = 0; r < kTile / 4; ++r) {
+    const int t = t0 + ty + 4 * r, h = h0 + tx;
+    float v = 0.f;
+    if (t < a.C && h < a.H) {
+      v = static_cast<float>(pd[(int64_t)t * a.pd_stride + h]);
+      // bf16 * bf16 is exact in fp32: one rounding, as the reference's multiply
+      if (beta) v = static_cast<float>(round_to<T>(v * static_cast<float>(beta[t])));
+    }
+    tile[ty + 4 * r][tx] = v;
+  }
+  __syncthreads();
+  T* out = static_cast<T*>(a.pdt) + (int64_t)bk * a.H * a.C;
+#pragma unroll
+  for (int r = 0; r < kTile / 4; ++r) {
+    const int h = h0 + ty + 4 * r, t = t0 + tx;
+    if (h < a.H && t < a.C) out[(int64_t)h * a.C + t] = static_cast<T>(tile[tx][ty + 4 * r]);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store_tile_t(float (&tile)[kTile][kTile + 1], const float (&v)[16],
+                                             T* out, int h0, int i0, int H, int I, int tx,
+                                             int ty) {
+  // v[r] is element (h0 + ty + 4r, i0 + tx); out is (I, H): row i, column h
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 16; ++r) tile[ty + 4 * r][tx] = v[r];
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int i = i0 + ty + 4 * r, h = h0 + tx;
+    if (i < I && h < H) out[(int64_t)i * H + h] = static_cast<T>(tile[tx][ty + 4 * r]);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void ttt_scan_kernel(TttScanArgs a) {
+  __shared__ float tile[kTile][kTile + 1];
+  const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;
+  const int i0 = blockIdx.x * kTile, h0 = blockIdx.y * kTile;
+  const int i = i0 + tx;
+  const T* wc = static_cast<const T*>(a.w_cur);
+  const T* dw = static_cast<const T*>(a.dw);
+  T* steps = static_cast<T*>(a.steps_t);
+  const int64_t HI = (int64_t)a.H * a.I;
+  float w[16], acc[16], ws[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int h = h0 + ty + 4 * r;
+    w[r] = (h < a.H && i < a.I) ? static_cast<float>(wc[(int64_t)h * a.I + i]) : 0.f;
+    acc[r] = 0.f;
+    ws[r] = w[r];
+  }
+  store_tile_t<T>(tile, w, steps, h0, i0, a.H, a.I, tx, ty);  // step 0: W_cur
+  for (int j = 0; j < a.nupd; ++j) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int h = h0 + ty + 4 * r;
+      const float d = (h < a.H && i < a.I) ? static_cast<float>(dw[j * HI + (int64_t)h * a.I + i])
+                                           : 0.f;
+      acc[r] = static_cast<float>(round_to<T>(acc[r] + d));          // running sum, stored
+      const float cs = static_cast<float>(round_to<T>(a.lr * acc[r]));  // lr * cumsum
+      ws[r] = static_cast<float>(round_to<T>(w[r] + cs));            // W_cur + cs_j
+    }
+    if (j + 1 < a.nsteps)
+      store_tile_t<T>(tile, ws, steps + (int64_t)(j + 1) * HI, h0, i0, a.H, a.I, tx, ty);
+  }
+  if (a.w_next != nullptr) {
+    T* wn = static_cast<T*>(a.w_next);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int h = h0 + ty + 4 * r;
+      if (h < a.H && i < a.I) wn[(int64_t)h * a.I + i] = static_cast<T>(ws[r]);
+    }
+  }
+}
+
+template <typename T>
+hipError_t launch_pdbt(const TttProjBetaArgs& a, hipStream_t st) {
+  const dim3 grid((a.H + kTile - 1) / kTile, (a.C + kTile - 1) / kTile, a.B * a.nupd);
+  hipLaunchKernelGGL(ttt_pd_beta_t_kernel<T>, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_scan(const TttScanArgs& a, hipStream_t st) {
+  const dim3 grid((a.I + kTile - 1) / kTile, (a.H + kTile - 1) / kTile, 1);
+  hipLaunchKernelGGL(ttt_scan_kernel<T>, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t rows, int cols,
@@ -250,6 +369,14 @@ hipError_t launch_ttt_features(const TttFeatureArgs& a, Elem dtype, Elem w_dtype
                                hipStream_t stream) {
   return dtype == Elem::BF16 ? launch_wt<__bf16>(a, w_dtype, stream)
                              : launch_wt<_Float16>(a, w_dtype, stream);
+}
+
+hipError_t launch_ttt_proj_beta_t(const TttProjBetaArgs& a, Elem dtype, hipStream_t stream) {
+  return dtype == Elem::BF16 ? launch_pdbt<__bf16>(a, stream) : launch_pdbt<_Float16>(a, stream);
+}
+
+hipError_t launch_ttt_scan(const TttScanArgs& a, Elem dtype, hipStream_t stream) {
+  return dtype == Elem::BF16 ? launch_scan<__bf16>(a, stream) : launch_scan<_Float16>(a, stream);
 }
 
 }  // namespace ttcd

@@ -297,7 +297,8 @@ class IPTTCDv9Prefill:
                 x, residual = _epi.rmsnorm(a_t, w[p + "mlp_norm.weight"], eps, residual=residual)
             y = _ttt.ttt_mlp(x, s, self.ttt[i], chunk=c["ttt_chunk"], lr=c["ttt_lr"],
                              update_every=c["ttt_update_every"], fused=self.fuse_extra,
-                             conv="kernel" if self.conv_kernel else "stock")
+                             conv="kernel" if self.conv_kernel else "stock",
+                             scan="kernel" if self.fuse_extra else "torch")
         else:
             o = _attn.window_attn(q, k, v, self.window_t)
             a = F.linear(o.reshape(B, T, -1), o_w)

@@ -147,6 +147,79 @@ def _stack_rows(x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
     return torch.cat([x.reshape(-1, H), t.reshape(-1, H)], dim=0)
 
 
+def proj_beta_t(pd: torch.Tensor, beta: torch.Tensor | None, B: int, nupd: int,
+                chunk: int) -> torch.Tensor:
+    """pd (B*nupd*chunk, H) -> (B*nupd, H, chunk) = per chunk (pd * beta)^T,
+    one rounding per element (scanfuse.py:126-127). beta: (B, >= nupd, chunk)
+    per-token learning rates or None."""
+    H = pd.shape[1]
+    if pd.dim() != 2 or pd.stride(1) != 1 or pd.shape[0] != B * nupd * chunk:
+        raise ValueError("proj_beta_t: pd must be (B*nupd*chunk, H) with a contiguous row")
+    bsb = 0
+    if beta is not None:
+        if beta.dim() != 3 or beta.shape[0] != B or beta.shape[1] < nupd or beta.shape[2] != chunk \
+                or not beta.is_contiguous() or beta.dtype != pd.dtype:
+            raise ValueError("proj_beta_t: beta must be contiguous (B, >= nupd, chunk) of pd's dtype")
+        bsb = beta.stride(0)
+    _check_gpu("proj_beta_t", pd=pd, beta=beta)
+    out = torch.empty(B * nupd, H, chunk, dtype=pd.dtype, device=pd.device)
+    _lib.check(_lib.lib().ttcd_ttt_proj_beta_t_fwd(
+        pd.data_ptr(), pd.stride(0), beta.data_ptr() if beta is not None else None, bsb,
+        out.data_ptr(), B, nupd, chunk, H, _DT[pd.dtype], _stream(pd)))
+    return out
+
+
+def scan_steps(dw: torch.Tensor | None, w_cur: torch.Tensor, lr: float, nsteps: int,
+               want_next: bool):
+    """One update group: dw (nupd, H, I) chunk updates, w_cur (H, I). Returns
+    (steps_t, w_next): steps_t (nsteps, I, H) with step 0 = w_cur^T and step s
+    = (w_cur + lr * cumsum(dw)[s-1])^T, every step rounded as torch's bf16 ops
+    round it (scanfuse.py:157-170); w_next = w_cur + lr * cumsum(dw)[-1] or
+    None."""
+    H, I = w_cur.shape
+    nupd = 0 if dw is None else dw.shape[0]
+    if dw is not None and (dw.shape[1:] != (H, I) or not dw.is_contiguous()
+                           or dw.dtype != w_cur.dtype):
+        raise ValueError("scan_steps: dw must be contiguous (nupd, H, I) of w_cur's dtype")
+    if not w_cur.is_contiguous():
+        raise ValueError("scan_steps: w_cur must be contiguous")
+    _check_gpu("scan_steps", dw=dw, w_cur=w_cur)
+    dt = w_cur.dtype
+    lr_q = float(torch.tensor(lr, dtype=dt).item())   # the learning rate as the dtype stores it
+    steps = torch.empty(nsteps, I, H, dtype=dt, device=w_cur.device)
+    w_next = torch.empty(H, I, dtype=dt, device=w_cur.device) if want_next else None
+    _lib.check(_lib.lib().ttcd_ttt_scan_fwd(
+        dw.data_ptr() if dw is not None else None, w_cur.data_ptr(), lr_q, steps.data_ptr(),
+        w_next.data_ptr() if w_next is not None else None, nupd, nsteps, H, I, _DT[dt],
+        _stream(w_cur)))
+    return steps, w_next
+
+
+def _scan_kernel(pd, beta, z4, zh4, W_base, out, *, lr, update_every):
+    """The group loop of scanfuse.py:121-172 on the update kernels and
+    batched GEMMs. pd (B*(nchunk-1)*C, H); z4 / zh4 (B, nchunk, C, I);
+    out (B, nchunk, C, H)."""
+    B, nchunk, C, I = z4.shape
+    K = nchunk - 1
+    pdt = proj_beta_t(pd, beta, B, K, C)               # (B*K, H, C)
+    G = max(1, min(nchunk, update_every))
+    W_base = W_base.contiguous()
+    for b in range(B):
+        # every chunk's update at once: (K, H, C) @ (K, C, I) -> (K, H, I)
+        dW = torch.bmm(pdt[b * K:(b + 1) * K], zh4[b, :K])
+        W_cur = W_base
+        for gs in range(0, nchunk, G):
+            ge = min(gs + G, nchunk)
+            upd_end = min(ge, K)
+            last = ge >= nchunk
+            steps, W_next = scan_steps(dW[gs:upd_end] if upd_end > gs else None, W_cur, lr,
+                                       ge - gs, want_next=not last and upd_end > gs)
+            # the group's outputs: (Kg, C, I) @ (Kg, I, H) -> (Kg, C, H)
+            torch.bmm(z4[b, gs:ge], steps, out=out[b, gs:ge])
+            if W_next is not None:
+                W_cur = W_next
+
+
 class TttMlpWeights:
     """The TTT MLP's parameters, named after the reference module's
     (custom_models/ipttcd/modeling_ipttcdv9.py:87-182)."""
@@ -171,7 +244,8 @@ def stock_conv(v: torch.Tensor, cw: torch.Tensor) -> torch.Tensor:
 
 
 def ttt_mlp(x: torch.Tensor, t: torch.Tensor, w: TttMlpWeights, *, chunk: int, lr: float,
-            update_every: int, fused: bool = True, conv: str = "kernel") -> torch.Tensor:
+            update_every: int, fused: bool = True, conv: str = "kernel",
+            scan: str = "kernel") -> torch.Tensor:
     """The TTT MLP forward for a prefill: x the teacher hidden states after
     mlp_norm, t the student's (B, L, H). Returns the MLP output (B, L, H).
 
@@ -186,7 +260,13 @@ def ttt_mlp(x: torch.Tensor, t: torch.Tensor, w: TttMlpWeights, *, chunk: int, l
     cumsum at its end. `fused=False` runs the feature pass as separate launches
     (swiglu, conv, subtraction) for A/B measurement, with the conv kernel
     (conv="kernel": identical results) or the reference's unpatched torch
-    conv (conv="stock")."""
+    conv (conv="stock"). scan="kernel" runs the update scan as the
+    reference's group loop does it but batched: one GEMM for pd, one kernel
+    for pd * beta (transposed per chunk), one batched GEMM for every chunk's
+    dW, and per group one scan kernel (bf16 running sum, lr * sum, W_cur + cs
+    for every chunk, transposed) and one batched GEMM for the group's outputs;
+    scan="torch" runs the reference's per-chunk torch ops (the same roundings;
+    the GEMMs' accumulation order may differ)."""
     from .conv import causal_dwconv_x
 
     B, L, H = x.shape
@@ -203,6 +283,8 @@ def ttt_mlp(x: torch.Tensor, t: torch.Tensor, w: TttMlpWeights, *, chunk: int, l
     gu_t, gu_s = gu[:rows], gu[rows:]
     if conv not in ("kernel", "stock"):
         raise ValueError(f"ttt_mlp: conv must be 'kernel' or 'stock', got {conv!r}")
+    if scan not in ("kernel", "torch"):
+        raise ValueError(f"ttt_mlp: scan must be 'kernel' or 'torch', got {scan!r}")
     if fused and conv == "kernel":
         z, z_hat, diff = ttt_features(gu_t, gu_s, w.conv_t, w.conv_s, B, nchunk, C)
     else:
@@ -233,7 +315,12 @@ def ttt_mlp(x: torch.Tensor, t: torch.Tensor, w: TttMlpWeights, *, chunk: int, l
         W_upd_t = W_base.t()
         if w.ttt_proj is not None:
             W_upd_t = torch.matmul(W_base.t(), w.ttt_proj)  # (I, H), scanfuse.py:95-96
-        pd = torch.mm(diff, W_upd_t).view(B, nchunk - 1, C, H)
+        pd = torch.mm(diff, W_upd_t)                  # (B*(nchunk-1)*C, H)
+        if scan == "kernel":
+            _scan_kernel(pd, beta, z4, z_hat.view(B, nchunk, C, I), W_base, out, lr=lr,
+                         update_every=update_every)
+            return out.view(B, nchunk * C, H)[:, :L]
+        pd = pd.view(B, nchunk - 1, C, H)
         if beta is not None:
             pd = pd * beta[:, :nchunk - 1, :, None]
         zh4 = z_hat.view(B, nchunk, C, I)
