@@ -186,11 +186,55 @@ def _rope(x, cos, sin):
     return prologue_ref.rope_ref(x, cos, sin, 0)
 
 
+def _positions(T: int, cu_seqlens) -> torch.Tensor:
+    """Rotary positions: 0..T-1, or restarting at every packed sequence
+    (fla's rotary with cu_seqlens)."""
+    if cu_seqlens is None:
+        return torch.arange(T)
+    pos = torch.empty(T, dtype=torch.long)
+    cu = [int(x) for x in cu_seqlens]
+    for a, b in zip(cu[:-1], cu[1:]):
+        pos[a:b] = torch.arange(b - a)
+    return pos
+
+
+def output_gate_ref(c: dict, w: dict, p: str, x, o, dt):
+    """fla Attention's output gate (fla/layers/attn.py:149-167, 284-292) on
+    o (B, T, H, D) with x the attn_norm output: g = x @ g_proj^T; with
+    gate_fn 'swish' and fuse_norm, FusedRMSNormGated: rmsnorm(o) * w * g *
+    sigmoid(g) in fp32, one rounding (fla/modules/fused_norm_gate.py:91-97);
+    otherwise g_norm (RMSNorm over D, stored) times gate_fn(g) (stored), a
+    rounded product. Returns (B, T, H*D)."""
+    B, T, Hh, D = o.shape
+    g = _mm(x, w[p + "attn.g_proj.weight"].t(), dt).view(B, T, Hh, D)
+    eps = c["norm_eps"]
+    if c["gate_fn"] == "swish" and c["fuse_norm"]:
+        of = o.double()
+        y = of * torch.rsqrt(of.pow(2).mean(-1, keepdim=True) + eps)
+        y = y * w[p + "attn.g_norm_swish_gate.weight"].double()
+        gd = g.double()
+        y = y * gd * torch.sigmoid(gd)
+        return y.to(dt).reshape(B, T, -1)
+    on = prologue_ref.rms_norm_ref(o, w[p + "attn.g_norm.weight"], eps)
+    gd = g.double()
+    act = torch.sigmoid(gd) if c["gate_fn"] == "sigmoid" else gd * torch.sigmoid(gd)
+    return (on.double() * act.to(dt).double()).to(dt).reshape(B, T, -1)
+
+
 def prefill_ref(cfg: dict, w: dict, input_ids: torch.Tensor, logits_to_keep: int = 1,
-                dt=torch.bfloat16) -> torch.Tensor:
+                dt=torch.bfloat16, attention_mask=None, cu_seqlens=None) -> torch.Tensor:
     """Logits (B, logits_to_keep, V) of the reference prefill on the CPU.
     cfg: a resolved config (ttcd_amd.ipttcdv9.resolve_config); w: the
-    parameters under the reference's state-dict names (CPU tensors)."""
+    parameters under the reference's state-dict names (CPU tensors).
+
+    attention_mask (B, T) 0/1 padding mask, cu_seqlens packed sequences
+    (B = 1): the reference's fallback path (modeling_ipttcdv9.py:562-574,
+    794-850). Every layer's attention (fla Attention, fla/layers/attn.py:
+    226-262) attends within each row's unpadded tokens or within each packed
+    sequence, with rotary positions restarting per packed sequence (not
+    shifted for padding: a prefill has no cache). The TTT student is
+    flash_attn_func on the whole padded / packed rows (:825-827), and the TTT
+    MLP runs on them as they are. Padded rows attend nowhere: o = 0."""
     c = cfg
     B, T = input_ids.shape
     H, I, D = c["hidden_size"], c["intermediate_size"], c["head_dim"]
@@ -199,14 +243,40 @@ def prefill_ref(cfg: dict, w: dict, input_ids: torch.Tensor, logits_to_keep: int
     rows_tab = max(T, c["max_position_embeddings"] or 0)
     inv = prologue_ref.inv_freq_ref(D, c["rope_theta"])
     cos, sin = prologue_ref.tables_ref(inv, rows_tab, dt)
+    pos = _positions(T, cu_seqlens)
+    cos, sin = cos[pos], sin[pos]
     Wt = c["window_size"] if c["window_size"] is not None else T
     Ws = c["ttt_visible_chunks"] * c["ttt_chunk"]
+    if attention_mask is not None and bool(attention_mask.all()):
+        attention_mask = None
 
     def norm(x, wt):
         return prologue_ref.rms_norm_ref(x, wt, eps)
 
     def attn(q, k, v, W):
         return attn_ref.band_reference(q, k, v, 0, W).to(dt)
+
+    def teacher_attn(q, k, v):
+        if attention_mask is not None:
+            o = torch.zeros_like(q)
+            for b in range(B):
+                idx = attention_mask[b].nonzero().flatten()
+                if idx.numel():
+                    o[b, idx] = attn(q[b:b + 1, idx], k[b:b + 1, idx], v[b:b + 1, idx], Wt)[0]
+            return o
+        if cu_seqlens is not None:
+            o = torch.zeros_like(q)
+            cu = [int(x) for x in cu_seqlens]
+            for a, e in zip(cu[:-1], cu[1:]):
+                if e > a:
+                    o[:, a:e] = attn(q[:, a:e], k[:, a:e], v[:, a:e], Wt)
+            return o
+        return attn(q, k, v, Wt)
+
+    def gated(p, x, o):
+        if c["use_output_gate"]:
+            return output_gate_ref(c, w, p, x, o, dt)
+        return o.reshape(B, T, -1)
 
     h = w["model.embeddings.weight"][input_ids].to(dt)
     for i in range(c["num_hidden_layers"]):
@@ -222,9 +292,9 @@ def prefill_ref(cfg: dict, w: dict, input_ids: torch.Tensor, logits_to_keep: int
         q, k = _rope(q, cos, sin), _rope(k, cos, sin)
         o_w = w[p + "attn.o_proj.weight"]
         ttt = i in c["ttt_layers"] and T >= c["ttt_chunk"]
-        a_t = _mm(attn(q, k, v, Wt).reshape(B, T, -1), o_w.t(), dt)
+        a_t = _mm(gated(p, x, teacher_attn(q, k, v)), o_w.t(), dt)
         if ttt:
-            a_s = _mm(attn(q, k, v, Ws).reshape(B, T, -1), o_w.t(), dt)
+            a_s = _mm(gated(p, x, attn(q, k, v, Ws)), o_w.t(), dt)
             x, residual, s = epilogue_ref.dual_residual_rms_norm_ref(
                 a_t, a_s, residual, w[p + "mlp_norm.weight"], eps)
             y = ttt_mlp_ref(c, w, p, x, s, dt)

@@ -185,7 +185,7 @@ def test_resolve_config_and_unsupported_options():
                                 "num_hidden_layers": 1})
     # modeling_ipttcdv9.py:98-102: 256 * ceil(1024 * 4 * 2 / 3 / 256)
     assert derived["intermediate_size"] == 2816 and derived["head_dim"] == 64
-    for bad in ({"use_output_gate": True}, {"ttt_weight_renorm": True}, {"use_muon": True},
+    for bad in ({"ttt_weight_renorm": True}, {"use_muon": True},
                 {"ttt_normalize_student_features": True}, {"qkv_bias": True},
                 {"fuse_norm": False}, {"ttt_scan_state_dtype": "fp32"},
                 {"ttt_scan_state_dtype": "BF16"}):
@@ -286,3 +286,48 @@ def test_python_layers_refuse_cpu_tensors():
         epilogue.rmsnorm(x, torch.ones(64), 1e-6)
     with pytest.raises(ValueError, match="GPU"):
         ttt.swiglu(x, x)
+
+
+def test_output_gate_config_rules():
+    # fla's g_proj has num_kv_heads * head_dim outputs: the gate needs MHA
+    with pytest.raises(ValueError):
+        M.resolve_config(dict(M.QWEN3_06B_SWA8K, use_output_gate=True))
+    c = M.resolve_config(dict(M.QWEN3_06B_SWA8K, use_output_gate=True, num_kv_heads=16))
+    assert c["gate_fn"] == "sigmoid"
+    with pytest.raises(NotImplementedError):
+        M.resolve_config(dict(M.QWEN3_06B_SWA8K, use_output_gate=True, num_kv_heads=16,
+                              gate_fn="relu"))
+    with pytest.raises(NotImplementedError):
+        M.resolve_config(dict(M.QWEN3_06B_SWA8K, use_l2_softmax=True))
+    w = M.init_weights(dict(TINY, num_kv_heads=4, use_output_gate=True, gate_fn="swish"), "cpu")
+    assert "model.layers.0.attn.g_proj.weight" in w
+    assert "model.layers.0.attn.g_norm_swish_gate.weight" in w
+
+
+def test_oracle_packed_sequences_equal_each_sequence_alone():
+    """The oracle's cu_seqlens path (per-sequence attention, rotary positions
+    restarting per sequence) on a TTT-free config gives each sequence the
+    logits of a prefill of that sequence alone."""
+    cfg = dict(TINY, ttt_layers=[], num_hidden_layers=2)
+    c = M.resolve_config(cfg)
+    w = M.init_weights(cfg, "cpu", seed=2)
+    ids = torch.randint(0, 1024, (1, 96), generator=torch.Generator().manual_seed(3))
+    cu = torch.tensor([0, 40, 96])
+    packed = R.prefill_ref(c, w, ids, 0, torch.float32, cu_seqlens=cu)
+    for a, b in ((0, 40), (40, 96)):
+        alone = R.prefill_ref(c, w, ids[:, a:b], 0, torch.float32)
+        torch.testing.assert_close(packed[:, a:b], alone, rtol=1e-4, atol=1e-4)
+
+
+def test_oracle_padding_mask_equals_unpadded_row_up_to_rope_positions():
+    """A right-padded row under the mask equals the same tokens alone (right
+    padding keeps the rotary positions), on a TTT-free config."""
+    cfg = dict(TINY, ttt_layers=[], num_hidden_layers=2)
+    c = M.resolve_config(cfg)
+    w = M.init_weights(cfg, "cpu", seed=4)
+    ids = torch.randint(0, 1024, (1, 80), generator=torch.Generator().manual_seed(5))
+    mask = torch.ones(1, 80, dtype=torch.long)
+    mask[0, 50:] = 0
+    masked = R.prefill_ref(c, w, ids, 0, torch.float32, attention_mask=mask)
+    alone = R.prefill_ref(c, w, ids[:, :50], 0, torch.float32)
+    torch.testing.assert_close(masked[:, :50], alone, rtol=1e-4, atol=1e-4)

@@ -303,3 +303,96 @@ def test_config5_full_size_paths_agree():
     _logits_close(got["fused"], got["stock"])
     _logits_close(got["patched"], got["stock"])
     _logits_close(got["fused"], got["patched"], max_frac=2e-2, mean_frac=1e-2)
+
+
+# ------------------------------------------------ fast-path gate and fallback
+
+def _ids(B, T, seed, vocab=1024):
+    return torch.randint(0, vocab, (B, T), generator=torch.Generator().manual_seed(seed))
+
+
+def test_disabled_fast_path_matches_fast_path_and_oracle(monkeypatch):
+    """IPTTCD_DISABLE_FAST_PREFILL=1 routes the TTT layers through the
+    reference's fallback (two windowed calls, two norms;
+    modeling_ipttcdv9.py:562-574, 794-850), which the reference calls bit-exact
+    with its fast path: here both match the oracle and each other."""
+    c = M.resolve_config(TINY)
+    w = M.init_weights(TINY, DEV, seed=4)
+    ids = _ids(1, 1024, 41)
+    fast = M.IPTTCDv9Prefill(TINY, w).forward(ids.to(DEV), logits_to_keep=8)
+    monkeypatch.setenv("IPTTCD_DISABLE_FAST_PREFILL", "1")
+    slow = M.IPTTCDv9Prefill(TINY, w).forward(ids.to(DEV), logits_to_keep=8)
+    torch.cuda.synchronize()
+    want = R.prefill_ref(c, {k: v.cpu() for k, v in w.items()}, ids, 8, torch.bfloat16)
+    _logits_close(slow, want)
+    _logits_close(fast, slow, max_frac=2e-2, mean_frac=1e-2)
+
+
+def test_padding_mask_takes_the_fallback_and_matches_oracle():
+    """A left-padded batch: every layer attends within each row's unpadded
+    tokens (fla Attention's varlen path), the TTT student over the whole
+    row, as the reference's fallback does."""
+    c = M.resolve_config(TINY)
+    w = M.init_weights(TINY, DEV, seed=5)
+    B, T = 2, 1024
+    ids = _ids(B, T, 51)
+    mask = torch.ones(B, T, dtype=torch.long)
+    mask[0, :200] = 0          # row 0 left-padded by 200 tokens
+    got = M.IPTTCDv9Prefill(TINY, w).forward(ids.to(DEV), logits_to_keep=8,
+                                             attention_mask=mask.to(DEV))
+    torch.cuda.synchronize()
+    want = R.prefill_ref(c, {k: v.cpu() for k, v in w.items()}, ids, 8, torch.bfloat16,
+                         attention_mask=mask)
+    _logits_close(got, want)
+    # a mask of ones is no mask: the fast path
+    ones = M.IPTTCDv9Prefill(TINY, w).forward(ids.to(DEV), logits_to_keep=8,
+                                              attention_mask=torch.ones_like(mask).to(DEV))
+    none = M.IPTTCDv9Prefill(TINY, w).forward(ids.to(DEV), logits_to_keep=8)
+    torch.cuda.synchronize()
+    assert torch.equal(ones, none)
+
+
+def test_packed_sequences_take_the_fallback_and_match_oracle():
+    """cu_seqlens: three sequences packed in one row; attention within each,
+    rotary positions restarting per sequence, the TTT student over the row."""
+    c = M.resolve_config(TINY)
+    w = M.init_weights(TINY, DEV, seed=6)
+    ids = _ids(1, 1024, 61)
+    cu = torch.tensor([0, 300, 701, 1024], dtype=torch.int32)
+    got = M.IPTTCDv9Prefill(TINY, w).forward(ids.to(DEV), logits_to_keep=8,
+                                             cu_seqlens=cu.to(DEV))
+    torch.cuda.synchronize()
+    want = R.prefill_ref(c, {k: v.cpu() for k, v in w.items()}, ids, 8, torch.bfloat16,
+                         cu_seqlens=cu)
+    _logits_close(got, want)
+
+
+# MHA so that fla's g_proj (num_kv_heads * head_dim outputs) matches the output
+GATED = dict(TINY, num_kv_heads=4, use_output_gate=True)
+
+
+@pytest.mark.parametrize("gate_fn", ["sigmoid", "swish"])
+def test_output_gate_on_every_path_matches_oracle(gate_fn):
+    """use_output_gate (fla/layers/attn.py:284-292) on the stock, patched and
+    fused paths, and on the fallback. The reference's patched forward drops
+    the gate (strict xfail, test/test_fused_dual_attn.py:339-360); here every
+    path applies it to both attention outputs. gate_fn 'swish' with fuse_norm
+    is FusedRMSNormGated."""
+    cfg = dict(GATED, gate_fn=gate_fn)
+    c = M.resolve_config(cfg)
+    w = M.init_weights(cfg, DEV, seed=7)
+    # non-trivial gate norm weights
+    for key in list(w):
+        if key.endswith(("g_norm.weight", "g_norm_swish_gate.weight")):
+            w[key] = (1 + 0.3 * _rand(w[key].shape[0], seed=len(key))).to(DEV)
+    ids = _ids(1, 1024, 71)
+    want = R.prefill_ref(c, {k: v.cpu() for k, v in w.items()}, ids, 8, torch.bfloat16)
+    got = {p: M.IPTTCDv9Prefill(cfg, w, path=p).forward(ids.to(DEV), logits_to_keep=8)
+           for p in M.PATHS}
+    torch.cuda.synchronize()
+    for p in M.PATHS:
+        _logits_close(got[p], want)
+    # the gate matters: without it the logits move
+    plain = R.prefill_ref(dict(c, use_output_gate=False), {k: v.cpu() for k, v in w.items()},
+                          ids, 8, torch.bfloat16)
+    assert (plain.float() - want.float()).abs().mean() > 0.1 * want.float().abs().mean()

@@ -34,13 +34,30 @@ vs `--patch fused_conv`:
             GEMM over both outputs, one dual norm) and fused TTT feature pass.
 Everything outside the TTT layers is the same in all three.
 
-Not covered (raise NotImplementedError): use_output_gate, qkv_bias,
-non-causal TTT conv, ttt_weight_renorm, Muon, normalised TTT features or
-proj-diff, ttt_output_use_teacher_conv, a KV cache (prefill only; the
+Fast path and fallback (`_use_fast_prefill_path`, modeling_ipttcdv9.py:
+562-574): forward() takes the reference's padding `attention_mask` (B, T)
+and packed `cu_seqlens` (B = 1). With either (a mask with a zero), or with
+IPTTCD_DISABLE_FAST_PREFILL=1, the TTT layers take the reference's fallback
+(:794-850): the teacher and student as two windowed calls, two o_proj GEMMs
+and two norms. With a mask or cu_seqlens every layer's attention runs within
+each row's unpadded tokens / each packed sequence (fla Attention's varlen
+path, fla/layers/attn.py:226-262, on this package's varlen kernel), rotary
+positions restart per packed sequence, and the TTT student attends over the
+whole rows as the reference's flash_attn_func call does (:825-827).
+
+The output gate (use_output_gate, fla/layers/attn.py:149-167, 284-292) is
+applied to both attention outputs on every path, including the patched one,
+where the reference's patch drops it (a strict xfail,
+test/test_fused_dual_attn.py:339-360).
+
+Not covered (raise NotImplementedError): qkv_bias, non-causal TTT conv,
+ttt_weight_renorm, Muon, normalised TTT features or proj-diff,
+ttt_output_use_teacher_conv, l2 softmax, a KV cache (prefill only; the
 reference's cache writes are copies of k and v).
 """
 from __future__ import annotations
 
+import os
 
 import torch
 import torch.nn.functional as F
@@ -83,7 +100,8 @@ _DEFAULTS = {
     "ttt_visible_chunks": 1, "use_muon": False, "ttt_weight_renorm": False,
     "ttt_norm_proj_diff": False, "ttt_normalize_student_features": True,
     "ttt_update_every": 4, "ttt_fuse_proj_into_update": True, "fuse_norm": True,
-    "ttt_scan_state_dtype": "compute",
+    "ttt_scan_state_dtype": "compute", "gate_fn": "sigmoid", "elementwise_affine": True,
+    "use_l2_softmax": False,
 }
 
 
@@ -104,7 +122,8 @@ def resolve_config(cfg: dict) -> dict:
     c["ttt_teacher_conv"] = bool(c["ttt_teacher_conv"])
     c["ttt_student_conv"] = bool(c["ttt_student_conv"])
     unsupported = [k for k, bad in (
-        ("use_output_gate", c["use_output_gate"]), ("qkv_bias", c["qkv_bias"]),
+        ("qkv_bias", c["qkv_bias"]), ("use_l2_softmax", c["use_l2_softmax"]),
+        ("gate_fn", c["use_output_gate"] and c["gate_fn"] not in ("sigmoid", "swish", "silu")),
         ("ttt_conv_causal=False", c["ttt_layers"] and not c["ttt_conv_causal"]),
         ("ttt_weight_renorm", c["ttt_weight_renorm"]), ("use_muon", c["use_muon"]),
         ("ttt_normalize_student_features", c["ttt_layers"] and c["ttt_normalize_student_features"]),
@@ -120,7 +139,17 @@ def resolve_config(cfg: dict) -> dict:
     ) if bad]
     if unsupported:
         raise NotImplementedError(f"ipttcdv9 prefill: unsupported options {unsupported}")
+    if c["use_output_gate"] and c["num_kv_heads"] != c["num_heads"]:
+        # fla's g_proj has kv_dim outputs (fla/layers/attn.py:151): the gate
+        # multiplies the (num_heads * head_dim) output only when they match
+        raise ValueError("use_output_gate needs num_kv_heads == num_heads (g_proj outputs "
+                         "num_kv_heads * head_dim, the attention output num_heads * head_dim)")
     return c
+
+
+def _fused_gate(c: dict) -> bool:
+    """FusedRMSNormGated (swish gate with fuse_norm, fla/layers/attn.py:152-158)."""
+    return c["gate_fn"] == "swish" and c["fuse_norm"]
 
 
 def init_weights(cfg: dict, device, dtype=torch.bfloat16, seed: int = 0) -> dict:
@@ -153,6 +182,11 @@ def init_weights(cfg: dict, device, dtype=torch.bfloat16, seed: int = 0) -> dict
         if c["qk_norm"]:
             w[p + "attn.q_norm.weight"] = ones(D)
             w[p + "attn.k_norm.weight"] = ones(D)
+        if c["use_output_gate"]:
+            w[p + "attn.g_proj.weight"] = normal(Hkv * D, H)
+            if c["elementwise_affine"]:
+                gname = "g_norm_swish_gate" if _fused_gate(c) else "g_norm"
+                w[p + f"attn.{gname}.weight"] = ones(D)
         w[p + "mlp_norm.weight"] = ones(H)
         w[p + "mlp.gate_proj.weight"] = normal(I, H)
         w[p + "mlp.up_proj.weight"] = normal(I, H)
@@ -239,7 +273,7 @@ class IPTTCDv9Prefill:
 
     # ------------------------------------------------------------------ layers
 
-    def _qkv(self, i: int, x: torch.Tensor):
+    def _qkv(self, i: int, x: torch.Tensor, ctx: "_Prefill"):
         c, w = self.cfg, self.w
         B, T, _ = x.shape
         Hq, Hkv, D = self.Hq, self.Hkv, self.D
@@ -248,7 +282,7 @@ class IPTTCDv9Prefill:
         k = qkv[..., Hq * D:(Hq + Hkv) * D].view(B, T, Hkv, D)
         v = qkv[..., (Hq + Hkv) * D:].view(B, T, Hkv, D)
         p = f"model.layers.{i}.attn."
-        cos, sin = self.tables(T)
+        cos, sin = ctx.tables if ctx.tables is not None else self.tables(T)
         qw = w.get(p + "q_norm.weight") if c["qk_norm"] else None
         kw = w.get(p + "k_norm.weight") if c["qk_norm"] else None
         # fla's RMSNorm default eps for q_norm / k_norm (fla/layers/attn.py:61-63)
@@ -261,6 +295,50 @@ class IPTTCDv9Prefill:
             return "stock"
         return "fused" if self.fuse_extra else "patched"
 
+    def _teacher_attention(self, q, k, v, ctx: "_Prefill"):
+        """The teacher window within each row's unpadded tokens / each packed
+        sequence (fla Attention's varlen path) or over whole rows."""
+        if ctx.cu_seqlens is None:
+            return _attn.window_attn(q, k, v, self.window_t)
+        B, T, Hq, D = q.shape
+        W = self.window_t if self.window_t >= 0 else ctx.max_seqlen
+        if ctx.indices is None:  # packed sequences, B = 1
+            o = _attn.band_attn_varlen(q[0], k[0], v[0], ctx.cu_seqlens, ctx.max_seqlen, 0, W)
+            return o.view(B, T, Hq, D)
+        idx = ctx.indices
+        o = torch.zeros(B * T, Hq, D, dtype=q.dtype, device=q.device)
+        o[idx] = _attn.band_attn_varlen(
+            q.reshape(B * T, Hq, D)[idx], k.reshape(B * T, -1, D)[idx],
+            v.reshape(B * T, -1, D)[idx], ctx.cu_seqlens, ctx.max_seqlen, 0, W)
+        return o.view(B, T, Hq, D)
+
+    def _gate(self, i: int, x: torch.Tensor, o: torch.Tensor) -> torch.Tensor:
+        """The attention output gate (fla/layers/attn.py:284-292) on o
+        (B, T, H, D) with x the attn_norm output; returns (B, T, H*D)."""
+        B, T = o.shape[0], o.shape[1]
+        if not self.cfg["use_output_gate"]:
+            return o.reshape(B, T, -1)
+        c, w = self.cfg, self.w
+        p = f"model.layers.{i}.attn."
+        D = self.D
+        g = F.linear(x, w[p + "g_proj.weight"])
+        if _fused_gate(c):
+            # FusedRMSNormGated: rmsnorm(o) * w * g * sigmoid(g) in fp32, one
+            # rounding (fla/modules/fused_norm_gate.py:91-95)
+            of = o.float()
+            y = of * torch.rsqrt(of.pow(2).mean(-1, keepdim=True) + c["norm_eps"])
+            nw = w.get(p + "g_norm_swish_gate.weight")
+            if nw is not None:
+                y = y * nw.float()
+            gf = g.float().view(B, T, -1, D)
+            return (y * gf * torch.sigmoid(gf)).to(o.dtype).reshape(B, T, -1)
+        nw = w.get(p + "g_norm.weight")
+        if nw is None:
+            nw = torch.ones(D, dtype=o.dtype, device=o.device)
+        on = _epi.rmsnorm(o.reshape(-1, D).contiguous(), nw, c["norm_eps"]).view(B, T, -1)
+        act = torch.sigmoid(g) if c["gate_fn"] == "sigmoid" else F.silu(g)
+        return on * act
+
     def _ttt_attention(self, q, k, v):
         if self.attn_kernel == "triton":
             return _attn.fused_dual_window_attn(q, k, v, self.window_t, self.window_s)
@@ -269,7 +347,8 @@ class IPTTCDv9Prefill:
         return (_attn.window_attn(q, k, v, self.window_t),
                 _attn.window_attn(q, k, v, self.window_s))
 
-    def layer(self, i: int, h: torch.Tensor, y_prev: torch.Tensor | None = None):
+    def layer(self, i: int, h: torch.Tensor, y_prev: torch.Tensor | None = None,
+              ctx: "_Prefill | None" = None):
         """One block. With y_prev, the block input is h + y_prev (the previous
         block's closing residual add), fused with this block's attn_norm.
         Returns (residual, y): the block output is residual + y."""
@@ -277,18 +356,30 @@ class IPTTCDv9Prefill:
         p = f"model.layers.{i}."
         eps = c["norm_eps"]
         B, T, H = h.shape
+        ctx = ctx if ctx is not None else _Prefill()
         if y_prev is None:
             residual = h
             x = _epi.rmsnorm(h, w[p + "attn_norm.weight"], eps)
         else:
             x, residual = _epi.add_rmsnorm(y_prev, h, w[p + "attn_norm.weight"], eps)
-        q, k, v = self._qkv(i, x)
+        xa = x  # attn_norm output: the gate's input
+        q, k, v = self._qkv(i, x, ctx)
         o_w = w[p + "attn.o_proj.weight"]
+        gated = c["use_output_gate"]
         if i in self.ttt and T >= c["ttt_chunk"]:
             norm = _NormView(w[p + "mlp_norm.weight"], eps)
             proj = _LinearView(o_w)
-            o_t, o_s = self._ttt_attention(q, k, v)
-            if self.fuse_extra:
+            if ctx.fast:
+                o_t, o_s = self._ttt_attention(q, k, v)
+            else:
+                # the reference's fallback (modeling_ipttcdv9.py:794-850): the
+                # teacher through the (unpad-aware) attention, the student a
+                # windowed call on the whole rows
+                o_t = self._teacher_attention(q, k, v, ctx)
+                o_s = _attn.window_attn(q, k, v, self.window_s)
+            if gated:
+                o_t, o_s = self._gate(i, xa, o_t), self._gate(i, xa, o_s)
+            if self.fuse_extra and ctx.fast:
                 x, residual, s = _epi.fused_attn_epilogue(proj, norm, o_t, o_s, residual)
             else:
                 a_t = F.linear(o_t.reshape(B, T, -1), o_w)
@@ -300,23 +391,65 @@ class IPTTCDv9Prefill:
                              conv="kernel" if self.conv_kernel else "stock",
                              scan="kernel" if self.fuse_extra else "torch")
         else:
-            o = _attn.window_attn(q, k, v, self.window_t)
-            a = F.linear(o.reshape(B, T, -1), o_w)
+            o = self._teacher_attention(q, k, v, ctx)
+            a = F.linear(self._gate(i, xa, o), o_w)
             x, residual = _epi.rmsnorm(a, w[p + "mlp_norm.weight"], eps, residual=residual)
             y = _ttt.swiglu_mlp(x, self.gu_w[i], w[p + "mlp.down_proj.weight"])
         return residual, y
 
+    def _prefill_context(self, B: int, T: int, attention_mask, cu_seqlens) -> "_Prefill":
+        """_use_fast_prefill_path (modeling_ipttcdv9.py:562-574) and what the
+        fallback needs: unpad indices and cu_seqlens for a padding mask,
+        per-sequence rotary tables for packed sequences."""
+        ctx = _Prefill()
+        if attention_mask is not None:
+            if attention_mask.shape != (B, T):
+                raise ValueError(f"attention_mask must be (B, T) = ({B}, {T}), got "
+                                 f"{tuple(attention_mask.shape)}")
+            m = attention_mask.to(self.dev).bool()
+            if not bool(m.all()):  # a host sync, as the reference's gate makes
+                if cu_seqlens is not None:
+                    raise ValueError("pass either a padding attention_mask or cu_seqlens")
+                lens = m.sum(1, dtype=torch.int32)
+                ctx.indices = m.reshape(-1).nonzero().flatten()
+                ctx.cu_seqlens = F.pad(torch.cumsum(lens, 0, dtype=torch.int32), (1, 0))
+                ctx.max_seqlen = int(lens.max().item())
+        if cu_seqlens is not None:
+            if B != 1:
+                raise ValueError("cu_seqlens needs a packed batch of one row (B = 1)")
+            cu = torch.as_tensor(cu_seqlens, dtype=torch.int32, device=self.dev)
+            cu_h = cu.cpu()
+            if cu_h[0] != 0 or int(cu_h[-1]) != T or bool((cu_h[1:] < cu_h[:-1]).any()):
+                raise ValueError("cu_seqlens must rise from 0 to T")
+            ctx.cu_seqlens = cu
+            ctx.max_seqlen = int((cu_h[1:] - cu_h[:-1]).max().item())
+            # rotary positions restart at every sequence (fla's varlen rotary)
+            seq = torch.repeat_interleave(torch.arange(cu_h.numel() - 1, device=self.dev),
+                                          (cu[1:] - cu[:-1]).long())
+            pos = torch.arange(T, device=self.dev) - cu[:-1].long()[seq]
+            cos, sin = self.tables(T)
+            ctx.tables = (cos[pos].contiguous(), sin[pos].contiguous())
+        ctx.fast = (os.environ.get("IPTTCD_DISABLE_FAST_PREFILL") != "1"
+                    and ctx.cu_seqlens is None)
+        return ctx
+
     @torch.inference_mode()
-    def forward(self, input_ids: torch.Tensor, logits_to_keep: int = 1) -> torch.Tensor:
+    def forward(self, input_ids: torch.Tensor, logits_to_keep: int = 1,
+                attention_mask: torch.Tensor | None = None,
+                cu_seqlens: torch.Tensor | None = None) -> torch.Tensor:
         """Logits (B, logits_to_keep, vocab) of the prefill of `input_ids`
         (B, T), as IPTTCDForCausalLM(input_ids, logits_to_keep=...) returns them
-        with fuse_linear_cross_entropy off (bench_prefill.py:73-74)."""
+        with fuse_linear_cross_entropy off (bench_prefill.py:73-74).
+        attention_mask: the (B, T) 0/1 padding mask; cu_seqlens: packed
+        sequences of a (1, T) batch (int32, 0 .. T)."""
         if input_ids.dim() != 2 or input_ids.device != self.dev:
             raise ValueError("input_ids must be (B, T) on the model's device")
+        B, T = input_ids.shape
+        ctx = self._prefill_context(B, T, attention_mask, cu_seqlens)
         h = F.embedding(input_ids, self.w["model.embeddings.weight"])
         y = None
         for i in range(self.cfg["num_hidden_layers"]):
-            h, y = self.layer(i, h, y)
+            h, y = self.layer(i, h, y, ctx)
         if logits_to_keep > 0:  # only the kept rows of the last block's output
             h, y = h[:, -logits_to_keep:], y[:, -logits_to_keep:]
         keep = h + y
@@ -340,6 +473,17 @@ def patch_triton_conv(model: IPTTCDv9Prefill) -> int:
     chunk-local conv kernel instead of the rearranged torch conv."""
     model.conv_kernel = True
     return len(model.ttt)
+
+
+class _Prefill:
+    """Per-forward state of the fast-path gate and the fallback."""
+
+    def __init__(self):
+        self.fast = True          # _use_fast_prefill_path
+        self.indices = None       # unpadded token rows of a padded batch
+        self.cu_seqlens = None    # int32 sequence starts (unpadded rows or packed)
+        self.max_seqlen = 0
+        self.tables = None        # per-token rotary rows for packed sequences
 
 
 class _NormView:
