@@ -91,8 +91,11 @@ ttcd_status ttcd_band_attn_fwd(
 /*
  * rescale_log2 (the calls below that take it; the two above use 8): the
  * online softmax keeps a reference row max and moves it, rescaling the
- * partial output, only when a row's max exceeds it by more than
- * 2^rescale_log2. 8 (lazy) is the fastest. 0 keeps the exact running max of
+ * partial output, only when the probabilities against it could exceed
+ * 2^rescale_log2: at head_dim 64 when a row's max exceeds it by more than
+ * 2^rescale_log2, at head_dim 128 when a 64-key tile's probabilities over a
+ * half row (32 keys) sum above 2^rescale_log2. Either way every probability
+ * stays <= 2^rescale_log2. 8 (lazy) is the fastest. 0 keeps the exact running max of
  * the reference kernel (fused_dual_attn.py:100-107), whose numerics it then
  * follows: at config 1, 98.6 % (teacher) and 99.96 % (student) of the bf16
  * outputs are bit-identical to a CPU emulation of the reference kernel, vs

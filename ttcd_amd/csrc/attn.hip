@@ -32,7 +32,9 @@
 //   * Software pipeline inside each wavefront: while the MFMAs of the next
 //     slot's scores S(k+1) run, the VALU computes exp2 of S(k); the PV MFMAs
 //     of slot k then run while the VALU sums the row of S(k) and reduces the
-//     row max of S(k+1).
+//     row max of S(k+1) (slot_body). In the lazy mode at D = 128 no row max
+//     is needed before the exp2, so the PV MFMAs of slot k run under the
+//     first half of S(k+1)'s exp2 instead (slot_body_lazy).
 //   * Workgroups are remapped so each XCD (own L2) sweeps a contiguous run of
 //     (b, kv head, query block, head in group); heaviest query blocks first.
 //   * Packed sequences (cu_seqlens): each workgroup builds its sequence's
@@ -43,9 +45,13 @@
 // raw-domain running max, p = exp2(s*c - m*c) with c = sm_scale*log2(e),
 // the m == -inf -> 0 guard, P rounded to the input dtype before PV, l summed
 // from the unrounded fp32 p, epilogue acc * (1/l) rounded to nearest-even.
-// The running max used in exp2 moves only when a row's max grows by more than
-// 2^rescale_log2 (lazy rescale, default 2^8; softmax is invariant to it up to
-// rounding); rescale_log2 = 0 keeps the exact running max of the reference.
+// With rescale_log2 > 0 (lazy rescale, default 8) the reference max m used in
+// exp2 may lag a row's running max, with every p <= 2^rescale_log2; softmax
+// is invariant to m up to rounding. At D = 64 m moves when the row's max
+// grows by more than 2^rescale_log2; at D = 128 when a slot's probabilities
+// against m sum above 2^rescale_log2 over a half row (which bounds every p the
+// same way without taking the row max in every slot). rescale_log2 = 0 keeps
+// the exact running max of the reference.
 //
 // Built with -fno-honor-nans -mno-amdgpu-ieee (ttcd_amd/build.py): no value
 // here is NaN for finite inputs (masked scores are -inf, every test below is
@@ -121,6 +127,11 @@ __device__ __forceinline__ float xhalf_sum(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
                                                   false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ bool xhalf_any(bool v) {
+  const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (r[0] | r[1]) != 0;
 }
 
 // Workgroup id -> logical id such that XCD x (which receives ids g = x, x+8,
@@ -453,6 +464,125 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
   return fmaxf(mx0, mx1);
 }
 
+// Scores of a slot exp'd under the previous slot's PV MFMAs in the lazy mode
+// (the rest run under the slot's own score MFMAs).
+#ifndef TTCD_EA
+#define TTCD_EA 16
+#endif
+template <int D>
+constexpr int lazy_ea() {
+  return TTCD_EA;
+}
+
+// exp2 of score idx of s against mc, packed in pairs into P^T k-step idx / 8
+// of p, summed in idx order (even / odd chains, as the exact mode sums them).
+template <typename T>
+__device__ __forceinline__ void exp_one(const f32x16 (&s)[2], typename VecT<T>::v8 (&p)[4],
+                                        int idx, float c, float mc, float& pe, float& ps0,
+                                        float& ps1) {
+  const float v = fast_exp2(fmaf(score_at(s, idx), c, -mc));
+  if (idx & 1) {
+    p[idx >> 3][(idx & 7) - 1] = static_cast<T>(pe);
+    p[idx >> 3][idx & 7] = static_cast<T>(v);
+    ps1 = idx == 1 ? v : ps1 + v;
+  } else {
+    pe = v;
+    ps0 = idx == 0 ? v : ps0 + v;
+  }
+}
+
+// The slot of the lazy mode (rescale_log2 > 0). Each row keeps its reference
+// max m until a slot's probabilities against it leave the bound: the slot's
+// sum of p over a half-row (32 keys) exceeds 2^rescale_log2 (so every p stays
+// <= 2^rescale_log2, the exact mode's bound), or the row has no reference
+// yet. No row max is taken in the common path: rescue() takes it in the rare
+// slot that crosses the bound, and that slot's exp2 are redone against the
+// new reference. The exp2 of a slot need no max first, so they are split
+// over two slots' MFMAs. Issue order:
+//   phase 1: the scores S(k+1) (2*DK MFMAs), K operand reads R1 ahead, with
+//            the exp2 / packing / row sums of S(k) scores EA .. 31 between
+//            them (scores 0 .. EA-1 ran in the previous slot). side(i) runs
+//            after MFMA i.
+//   check:   rescue(lane sum, mc): one compare and a wave-uniform branch in
+//            the common path. It moves the references of the rows out of
+//            bound, rescales O^T and l, and returns true if S(k) must be
+//            redone; then l += the slot's sums.
+//   phase 2: PV(k) (4*DT MFMAs) from pc, V^T reads R2 ahead, with the exp2 of
+//            S(k+1) scores 0 .. EA-1 into pn, against pre_next() (which masks
+//            S(k+1) if needed and returns its m*c, +inf for a skipped slot).
+// mc and ps0 / ps1 / pe carry the next slot's exp2 state across the call.
+template <int D, typename T, typename PreNext, typename Rescue, typename Side>
+__device__ __forceinline__ void slot_body_lazy(const Ctx<D, T>& x, f32x16 (&sc)[2],
+                                               f32x16 (&sn)[2], typename VecT<T>::v8 (&pc)[4],
+                                               typename VecT<T>::v8 (&pn)[4],
+                                               f32x16 (&o)[Geo<D>::DT], float& l, float& mc,
+                                               float& ps0, float& ps1, float& pe,
+                                               const LDS_AS char* kb, const LDS_AS char* vbase,
+                                               PreNext&& pre_next, Rescue&& rescue, Side&& side) {
+  using G = Geo<D>;
+  using v8 = typename VecT<T>::v8;
+  constexpr int N1 = 2 * G::DK;
+  constexpr int N2 = 4 * G::DT;
+  constexpr int R1 = TTCD_R1;
+  constexpr int R2 = TTCD_R2;
+  constexpr int EA = lazy_ea<D>();
+  static_assert(EA >= 0 && EA <= 32, "scores per phase");
+
+  uint32_t xk = x.ln.xk;
+  asm volatile("" : "+v"(xk));
+  const LDS_AS char* vb[G::DT];
+#pragma unroll
+  for (int dt = 0; dt < G::DT; ++dt) {
+    uint32_t a = x.ln.vb[dt];
+    asm volatile("" : "+v"(a));
+    vb[dt] = vbase + a;
+  }
+
+  // phase 1
+  v8 ka[N1];
+#pragma unroll
+  for (int i = 0; i < R1; ++i) ka[i] = read_k<D, T>(kb, xk, i);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < N1; ++i) {
+    const int kt = i & 1, ks = i >> 1;
+    sn[kt] = mfma32(ka[i], x.qf[ks], i < 2 ? f32x16{} : sn[kt]);
+    if (i + R1 < N1) ka[i + R1] = read_k<D, T>(kb, xk, i + R1);
+    const int e0 = EA + (32 - EA) * i / N1, e1 = EA + (32 - EA) * (i + 1) / N1;
+#pragma unroll
+    for (int idx = e0; idx < e1; ++idx) exp_one<T>(sc, pc, idx, x.c, mc, pe, ps0, ps1);
+    // keep the sums here, in the MFMA shadow (otherwise they sink to the check)
+    asm volatile("" : "+v"(ps0), "+v"(ps1));
+    side(i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  if (__builtin_expect(rescue(ps0 + ps1, mc), 0)) {
+#pragma unroll
+    for (int idx = 0; idx < 32; ++idx) exp_one<T>(sc, pc, idx, x.c, mc, pe, ps0, ps1);
+  }
+  l += ps0 + ps1;
+  mc = pre_next();
+  ps0 = ps1 = 0.f;
+
+  // phase 2
+  v8 vt[N2];
+#pragma unroll
+  for (int i = 0; i < R2; ++i) vt[i] = read_vt<D, T>(vb[i % G::DT], i / G::DT);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < N2; ++i) {
+    const int ks = i / G::DT, dt = i % G::DT;
+    o[dt] = mfma32(vt[i], pc[ks], o[dt]);
+    const int e0 = EA * i / N2, e1 = EA * (i + 1) / N2;
+#pragma unroll
+    for (int idx = e0; idx < e1; ++idx) exp_one<T>(sn, pn, idx, x.c, mc, pe, ps0, ps1);
+    asm volatile("" : "+v"(ps0), "+v"(ps1));
+    if (i + R2 < N2) vt[i + R2] = read_vt<D, T>(vb[(i + R2) % G::DT], (i + R2) / G::DT);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Per-wave view of one slot of the workgroup's plan.
 struct SlotInfo {
   int j0;     // first key of the slot's tile
@@ -492,7 +622,7 @@ constexpr int waves_per_simd() {
   return D == 64 ? TTCD_D64_WAVES : 2;
 }
 
-template <int D, typename T, bool DUAL>
+template <int D, typename T, bool DUAL, bool LAZY>
 __global__ __attribute__((amdgpu_flat_work_group_size(kWaves * 64, kWaves * 64),
                           amdgpu_waves_per_eu(waves_per_simd<D>(), waves_per_simd<D>())))
 void attn_fwd_kernel(AttnArgs a) {
@@ -606,8 +736,14 @@ void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int dt = 0; dt < G::DT; ++dt) o[dt] = f32x16{};
   float m = -INFINITY, l = 0.f;
+  float mc_ref = 0.f;  // lazy mode: m*c, 0 while the row has no reference
+  const float bound = LAZY ? exp2f(a.rescale_log2) : 0.f;
   bool emitted_s = false;
   f32x16 s0[2], s1[2];
+  // lazy mode: P^T of two consecutive slots, and the exp2 state carried from
+  // a slot's PV phase into the next slot
+  v8 pa[4], pb[4];
+  float lz_mc = 0.f, lz_ps0 = 0.f, lz_ps1 = 0.f, lz_pe = 0.f;
 
   // Two stages; stage k % 2 holds K(k) and V(k). In slot k the scores read
   // K(k+1) and PV reads V(k), so K(k+2) can replace K(k) (read in slot k-1)
@@ -634,20 +770,30 @@ void attn_fwd_kernel(AttnArgs a) {
   SlotInfo cur = slot_info(sc, wsl, n0, rep0, wave_valid && nslot > 0);
   // Scores of slot 0 and their lane max (unmasked; slot 0's mask and
   // reference max are settled inside the first slot).
-  float mx_lane;
+  float mx_lane = -INFINITY;
   {
     s0[0] = f32x16{};
     s0[1] = f32x16{};
 #pragma unroll
     for (int i = 0; i < 2 * G::DK; ++i)
       s0[i & 1] = mfma32(read_k<D, T>(x.lds, x.ln.xk, i), x.qf[i >> 1], s0[i & 1]);
-    float a0 = -INFINITY, a1 = -INFINITY;
+    if constexpr (!LAZY) {
+      float a0 = -INFINITY, a1 = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      a0 = fmaxf(a0, s0[0][e]);
-      a1 = fmaxf(a1, s0[1][e]);
+      for (int e = 0; e < 16; ++e) {
+        a0 = fmaxf(a0, s0[0][e]);
+        a1 = fmaxf(a1, s0[1][e]);
+      }
+      mx_lane = fmaxf(a0, a1);
     }
-    mx_lane = fmaxf(a0, a1);
+  }
+  if constexpr (LAZY) {
+    // slot 0's first exp2 (the later slots' run under the previous PV)
+    if (__builtin_expect(cur.mask, 0)) mask_band(s0, x.qrow, cur.j0, T_, cur.band, x.half);
+    lz_mc = cur.act != kSkip ? mc_ref : INFINITY;
+#pragma unroll
+    for (int idx = 0; idx < lazy_ea<D>(); ++idx)
+      exp_one<T>(s0, pa, idx, x.c, lz_mc, lz_pe, lz_ps0, lz_ps1);
   }
   // every wave has read K(0) before slot 0 replaces it with K(2)
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -657,7 +803,8 @@ void attn_fwd_kernel(AttnArgs a) {
   // slot runs the same code: a slot this wave skips folds all-zero
   // probabilities. Unrolled by two so the two score buffers swap roles
   // without register copies.
-  auto step = [&](f32x16 (&scur)[2], f32x16 (&snxt)[2], int k) __attribute__((always_inline)) {
+  auto step = [&](f32x16 (&scur)[2], f32x16 (&snxt)[2], v8 (&pcur)[4], v8 (&pnxt)[4], int k)
+                  __attribute__((always_inline)) {
     const int n2 = walk.n;
     const bool rep2 = walk.rep;
     if (k + 2 < nslot) dma_half(true, n2, k & 1);
@@ -700,8 +847,48 @@ void attn_fwd_kernel(AttnArgs a) {
     auto side = [&](int i) __attribute__((always_inline)) {
       if (i == 2) nxt = slot_info(sc, wsl, n1, rep1, wave_valid & (k + 1 < nslot));
     };
-    mx_lane = slot_body<D, T>(x, scur, snxt, o, l, x.lds + ((k + 1) & 1) * G::STAGE_B,
-                              x.lds + (k & 1) * G::STAGE_B + G::TILE_B, settle, side);
+    const LDS_AS char* kb = x.lds + ((k + 1) & 1) * G::STAGE_B;
+    const LDS_AS char* vbase = x.lds + (k & 1) * G::STAGE_B + G::TILE_B;
+    if constexpr (LAZY) {
+      // Mask S(k+1) if needed; m*c for its exp2 (+inf for a slot this wave
+      // skips).
+      auto pre_next = [&]() __attribute__((always_inline)) {
+        if (__builtin_expect(nxt.mask, 0)) mask_band(snxt, x.qrow, nxt.j0, T_, nxt.band, x.half);
+        return nxt.act != kSkip ? mc_ref : INFINITY;
+      };
+      // A row is out of bound when either half's sum t exceeds 2^rescale_log2
+      // or it has no reference yet. Such rows move their reference to their
+      // running max (O^T and l rescaled); the others keep theirs (alpha = 1,
+      // the same p), so a row's arithmetic depends on its own scores alone.
+      auto rescue = [&](float t, float& mc) __attribute__((always_inline)) {
+        const bool active = cur.act != kSkip;
+        const bool out = active & (!(t <= bound) | (m == -INFINITY));
+        if (__builtin_expect(__any(out) == 0, 1)) return false;
+        float a0 = -INFINITY, a1 = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          a0 = fmaxf(a0, scur[0][e]);
+          a1 = fmaxf(a1, scur[1][e]);
+        }
+        const float mx = xhalf_max(fmaxf(a0, a1));
+        const bool row_out = xhalf_any(out);
+        const float m_new = row_out ? fmaxf(m, mx) : m;
+        const bool grow = m_new > m;
+        const float mc_new = grow ? m_new * x.c : mc_ref;
+        const float alpha = grow ? fast_exp2(fmaf(m, x.c, -mc_new)) : 1.f;
+        l *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) o[dt] *= alpha;
+        m = grow ? m_new : m;
+        mc_ref = mc_new;
+        mc = mc_ref;
+        return true;
+      };
+      slot_body_lazy<D, T>(x, scur, snxt, pcur, pnxt, o, l, lz_mc, lz_ps0, lz_ps1, lz_pe, kb,
+                           vbase, pre_next, rescue, side);
+    } else {
+      mx_lane = slot_body<D, T>(x, scur, snxt, o, l, kb, vbase, settle, side);
+    }
     bool stored = false;
     if (DUAL && cur.act == kStudentLast) {
       T* os = static_cast<T*>(a.o_s) + o_base;
@@ -719,8 +906,8 @@ void attn_fwd_kernel(AttnArgs a) {
   };
 
   for (int k = 0; k < nslot; k += 2) {
-    step(s0, s1, k);
-    if (k + 1 < nslot) step(s1, s0, k + 1);
+    step(s0, s1, pa, pb, k);
+    if (k + 1 < nslot) step(s1, s0, pb, pa, k + 1);
   }
 
   if (wave_valid) {
@@ -739,8 +926,18 @@ template <int D, typename T, bool DUAL>
 hipError_t launch_typed(const AttnArgs& a, hipStream_t stream) {
   AttnArgs args = a;
   args.nwg = a.B * a.Hq * a.nqb;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, T, DUAL>), dim3(args.nwg), dim3(kWaves * 64), 0, stream,
-                     args);
+  // The sum-triggered lazy slot needs a second P^T buffer, which D = 64 has
+  // no registers for at three waves per SIMD; D = 64 and the exact mode take
+  // the max-first slot.
+  if constexpr (D == 128) {
+    if (a.rescale_log2 > 0.f) {
+      hipLaunchKernelGGL((attn_fwd_kernel<D, T, DUAL, true>), dim3(args.nwg), dim3(kWaves * 64),
+                         0, stream, args);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((attn_fwd_kernel<D, T, DUAL, false>), dim3(args.nwg), dim3(kWaves * 64), 0,
+                     stream, args);
   return hipGetLastError();
 }
 
