@@ -99,7 +99,7 @@ ttcd_status ttcd_band_attn_fwd(
  * the reference kernel (fused_dual_attn.py:100-107), whose numerics it then
  * follows: at config 1, 98.6 % (teacher) and 99.96 % (student) of the bf16
  * outputs are bit-identical to a CPU emulation of the reference kernel, vs
- * 58-61 % at 8, for ~5 % more time. Must lie in [0, 16] for BF16 and in
+ * 58-61 % at 8, for ~8 % more time. Must lie in [0, 16] for BF16 and in
  * [0, 15] for F16 (probabilities reach 2^rescale_log2 and are rounded to the
  * input dtype before PV; f16 overflows at 65520), else
  * TTCD_ERR_INVALID_ARGUMENT.

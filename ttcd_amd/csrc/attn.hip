@@ -467,7 +467,7 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
 // Scores of a slot exp'd under the previous slot's PV MFMAs in the lazy mode
 // (the rest run under the slot's own score MFMAs).
 #ifndef TTCD_EA
-#define TTCD_EA 16
+#define TTCD_EA 8
 #endif
 template <int D>
 constexpr int lazy_ea() {
