@@ -139,8 +139,9 @@ def cpu_baseline(q, k, v, cfg, target_s: float) -> dict:
     }
 
 
-def numerics_report() -> dict:
-    """Config 1 (B=1, T=2048, Hq=4, Hkv=2, D=64, 512/256): GPU vs fp32 oracle and the
+def numerics_report(D: int = 64) -> dict:
+    """Config 1 (B=1, T=2048, Hq=4, Hkv=2, D=64, 512/256; D=128 for the head
+    size whose lazy rescale follows the tile-sum rule): GPU vs fp32 oracle and the
     fraction of bf16 outputs bit-identical to a CPU emulation of the reference kernel,
     for the default lazy rescale and for exact_max=True (the reference's exact running
     max)."""
@@ -149,9 +150,9 @@ def numerics_report() -> dict:
     from ttcd_amd import fused_dual_window_attn
 
     g = torch.Generator().manual_seed(0)
-    q = torch.randn(1, 2048, 4, 64, generator=g).to(torch.bfloat16)
-    k = torch.randn(1, 2048, 2, 64, generator=g).to(torch.bfloat16)
-    v = torch.randn(1, 2048, 2, 64, generator=g).to(torch.bfloat16)
+    q = torch.randn(1, 2048, 4, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 2048, 2, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, 2048, 2, D, generator=g).to(torch.bfloat16)
     with torch.inference_mode():
         ot, os_ = fused_dual_window_attn(q.cuda(), k.cuda(), v.cuda(), 512, 256)
         xt, xs = fused_dual_window_attn(q.cuda(), k.cuda(), v.cuda(), 512, 256, exact_max=True)
@@ -579,6 +580,8 @@ def main() -> int:
         if not args.no_numerics:
             out["numerics_config1"] = numerics_report()
             log(f"numerics: {out['numerics_config1']}")
+            out["numerics_config1_d128"] = numerics_report(128)
+            log(f"numerics at D=128: {out['numerics_config1_d128']}")
     print(json.dumps(out), flush=True)
     return 0
 
