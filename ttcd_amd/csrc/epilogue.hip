@@ -26,6 +26,8 @@
 //
 // One wavefront per row: lane l owns the 16-byte chunks l, l + 64, ... of
 // the row, so every access is a coalesced 1 KiB transaction.
+// Activations are read once, with non-temporal loads; the weight row, shared
+// by every row, and the outputs, read by the next layer, stay cached.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -81,9 +83,9 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(
     V8<T> vt, vs, vr;
     vt.raw = vs.raw = vr.raw = u32x4{0u, 0u, 0u, 0u};
     if (ch < nch) {
-      vt.raw = *reinterpret_cast<const u32x4*>(a_t + base + 8 * ch);
-      if (DUAL) vs.raw = *reinterpret_cast<const u32x4*>(a_s + base + 8 * ch);
-      if (RES) vr.raw = *reinterpret_cast<const u32x4*>(res + base + 8 * ch);
+      vt.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a_t + base + 8 * ch));
+      if (DUAL) vs.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a_s + base + 8 * ch));
+      if (RES) vr.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(res + base + 8 * ch));
     }
     V8<T> ro;
 #pragma unroll

@@ -9,7 +9,7 @@
 // are copied from o_s bit for bit. o_s and o_t share strides; o_f has its
 // own (the LSE variant keeps it in a chunk-sized scratch). HBM-bound
 // elementwise pass: each thread moves 16 bytes of each operand with
-// coalesced vector accesses.
+// coalesced vector accesses, non-temporal loads for the partials (read once).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(MergeArgs a) {
   const int b = (int)(rest / a.T);
   const int64_t off = b * a.sb + t * a.st + h * a.sh + dg * 8;
   P8<T> s;
-  s.raw = *reinterpret_cast<const u32x4*>(os + off);
+  s.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(os + off));
   if (t < a.row_start) {
     *reinterpret_cast<u32x4*>(ot + off) = s.raw;
     return;
@@ -66,7 +66,8 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(MergeArgs a) {
     wf = expf(lf - lt);
   }
   P8<T> fv, out;
-  fv.raw = *reinterpret_cast<const u32x4*>(of + b * a.f_sb + t * a.f_st + h * a.f_sh + dg * 8);
+  fv.raw = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>(of + b * a.f_sb + t * a.f_st + h * a.f_sh + dg * 8));
 #pragma unroll
   for (int e = 0; e < 8; ++e)
     out.e[e] = static_cast<T>(fmaf(static_cast<float>(fv.e[e]), wf, static_cast<float>(s.e[e]) * wa));

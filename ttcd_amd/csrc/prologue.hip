@@ -23,7 +23,11 @@
 // and a wavefront handles 64 / (D/16) rows per step. Rows run over all q rows
 // (b, t, h) and then all k rows; consecutive rows of one token are
 // consecutive in memory, so every access of a wavefront is coalesced. The
-// cos/sin rows of a token are shared by all its heads (L1/L2 hits).
+// cos/sin rows of a token are shared by all its heads (L1/L2 hits); q and k
+// are read once, with non-temporal loads. The outputs are stored normally:
+// non-temporal stores measure 11 % faster for this kernel alone but make the
+// attention kernel that reads them next fetch them from HBM rather than the
+// 256 MiB last-level cache (the whole prefill 0.2-0.7 % slower at 32K).
 //
 // rope_table_kernel builds those tables as the reference does
 // (rotary.py:441-490 with pos_idx_in_fp32): freq = fp32(t) * inv_freq[i]
@@ -109,8 +113,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     x0.raw = x1.raw = u32x4{0u, 0u, 0u, 0u};
     c.raw = s.raw = u32x4{0u, 0u, 0u, 0u};
     if (valid) {
-      x0.raw = *reinterpret_cast<const u32x4*>(src + d0);
-      x1.raw = *reinterpret_cast<const u32x4*>(src + R + d0);
+      x0.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + d0));
+      x1.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + R + d0));
       const int64_t pos = (int64_t)t + a.offset;
       c.raw = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.cos) + pos * R + d0);
       s.raw = *reinterpret_cast<const u32x4*>(static_cast<const T*>(a.sin) + pos * R + d0);

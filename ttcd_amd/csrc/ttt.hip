@@ -3,6 +3,10 @@
 // swiglu_kernel replaces fla's swiglu_fwd_kernel (fla/modules/activations.py:
 // 412-426, called by swiglu / swiglu_linear in every MLP of the model):
 //   z = (g * s) * u,  s = 1 / (1 + exp(-g)),  in fp32, rounded to the dtype.
+// swiglu reads gate / up once, with non-temporal loads; the feature pass's
+// gate / up reads stay cached, since neighbouring runs re-read their halo
+// rows. Outputs are stored normally: the next op reads them soon, from the
+// last-level cache when they fit.
 //
 // ttt_features_kernel does, in one pass, what the TTT MLP's forward does in
 // five launches before its update GEMMs (custom_models/ipttcd/
@@ -85,8 +89,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ gate,
   const int64_t r = gid / ng;
   const int c = (int)(gid % ng) * 8;
   V8<T> g, u, o;
-  g.raw = *reinterpret_cast<const u32x4*>(gate + r * g_st + c);
-  u.raw = *reinterpret_cast<const u32x4*>(up + r * u_st + c);
+  g.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gate + r * g_st + c));
+  u.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(up + r * u_st + c));
 #pragma unroll
   for (int e = 0; e < 8; ++e)
     o.e[e] = round_to<T>(silu_mul(static_cast<float>(g.e[e]), static_cast<float>(u.e[e])));
@@ -180,7 +184,8 @@ __global__ __launch_bounds__(256) void ttt_features_kernel(
       df.e[e] = round_to<T>(static_cast<float>(tg.e[e]) - static_cast<float>(sh.e[e]));
     }
     *reinterpret_cast<u32x4*>(z_hat + row * I + d0) = sh.raw;
-    if (has_diff) *reinterpret_cast<u32x4*>(diff + (drow0 + c0 + r) * I + d0) = df.raw;
+    if (has_diff)
+      *reinterpret_cast<u32x4*>(diff + (drow0 + c0 + r) * I + d0) = df.raw;
 #pragma unroll
     for (int t = 0; t < K - 1; ++t)
 #pragma unroll
