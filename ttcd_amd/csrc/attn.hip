@@ -889,13 +889,11 @@ void attn_fwd_kernel(AttnArgs a) {
     } else {
       mx_lane = slot_body<D, T>(x, scur, snxt, o, l, kb, vbase, settle, side);
     }
-    bool stored = false;
     if (DUAL && cur.act == kStudentLast) {
       T* os = static_cast<T*>(a.o_s) + o_base;
       float* lse_s = a.lse_s ? a.lse_s + lse_base : nullptr;
       emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, q_off, lane);
       emitted_s = true;
-      stored = true;
     }
     cur = nxt;
     walk.advance();
