@@ -413,8 +413,9 @@ ttcd_status ttcd_ttt_scan_fwd(const void* dw, const void* w_cur, float lr, void*
  * is visited exactly once. Set dual = 0 for the single-band schedule, in
  * which case window_s = band_lo and window_t = band_hi. gqa_group is the
  * query-head group size Hq/Hkv (the current workgroup geometry, 128 tokens
- * of one head, does not depend on it). Also checks the kernel's incremental
- * slot walker and closed-form per-wave actions against the plan.
+ * of one head, does not depend on it). The pairs are counted from the
+ * per-slot words the kernel decodes (tile, action, band, mask, load bounds),
+ * each first checked against the plan and the per-tile predicates.
  */
 ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s,
                                         int window_t, int gqa_group,

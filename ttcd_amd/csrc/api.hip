@@ -909,42 +909,63 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
     if (!sc.wg_range(t0, t_last, &n_hi, &n_lo)) continue;
     auto r0_of_wave = [&](int wv) { return t0 + wv * kWaveRows; };
     const SlotPlan sp = make_slot_plan(sc, r0_of_wave, n_hi, n_lo);
-    if (sp.ndup > kWalkDup)
-      return fail(TTCD_ERR_UNSUPPORTED, "schedule error: %d repeated tiles > %d", sp.ndup, kWalkDup);
+    const int nslot = sp.slots();
     for (int w = 0; w < span / kWaveRows; ++w) {
       const int r0 = t0 + w * kWaveRows;
       if (r0 >= T) continue;
       bool student_done = false;
-      SlotWalker walk(sp);  // the kernel's incremental form of the plan
-      for (int k = 0; k < sp.slots(); ++k, walk.advance()) {
+      const WaveSlots ws(sc, r0);  // the kernel's closed form
+      // past the last slot the kernel's words load and fold nothing
+      for (int k = nslot; k < nslot + 2; ++k)
+        if (slot_word(sc, sp, ws, nslot, true, T, k) != 0)
+          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: word of slot %d past the end", k);
+      for (int k = 0; k < nslot; ++k) {
         bool repeat;
         const int n = sp.tile(k, &repeat);
-        if (walk.n != n || walk.rep != repeat)
-          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: walker (%d,%d) != plan (%d,%d) at slot %d",
-                      walk.n, (int)walk.rep, n, (int)repeat, k);
         const int j0 = sc.tile_start(n);
         const int act = slot_action(sc, r0, j0, repeat);
-        const WaveSlots ws(sc, r0);  // the kernel's closed form
         if (ws.act(n, repeat) != act)
           return fail(TTCD_ERR_UNSUPPORTED, "schedule error: closed-form action %d != %d (r0=%d n=%d)",
                       ws.act(n, repeat), act, r0, n);
+        // The kernel reads the slot only through its word: decode it and
+        // check every field against the plan and the per-tile predicates.
+        const uint32_t wd = slot_word(sc, sp, ws, nslot, true, T, k);
+        const bool interior = j0 >= 0 && j0 + kBlockN <= T;
+        if (n < 0 || word_tile(wd) != n || word_j0(sc, wd) != j0 || !(wd & kWordLoad) ||
+            ((wd & kWordInterior) != 0) != interior)
+          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: slot word tile/load (r0=%d k=%d)", r0, k);
+        if (slot_word(sc, sp, ws, nslot, false, T, k) != (wd & ~63u) + (wd & (kWordLoad | kWordInterior)))
+          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: idle-wave word (r0=%d k=%d)", r0, k);
+        const bool w_active = (wd & kWordActive) != 0;
+        if (w_active != (act != kSkip) ||
+            ((wd & kWordFar) != 0) != (act == kBand2 || act == kFar) ||
+            ((wd & kWordLast) != 0) != (act == kStudentLast))
+          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: slot word action (r0=%d k=%d)", r0, k);
         if (act != kSkip) {
           const Band b = (act == kBand2 || act == kFar) ? sc.p2 : sc.p1;
-          if (ws.mask(n, act) != !wave_full(r0, b, j0))
+          const Band wb = word_band(sc, wd);
+          if (wb.lo != b.lo || wb.hi != b.hi)
+            return fail(TTCD_ERR_UNSUPPORTED, "schedule error: slot word band (r0=%d n=%d)", r0, n);
+          const bool need_mask = !wave_full(r0, b, j0);
+          if (ws.mask(n, act) != need_mask || ((wd & kWordMask) != 0) != need_mask)
             return fail(TTCD_ERR_UNSUPPORTED, "schedule error: closed-form mask (r0=%d n=%d)", r0, n);
+        } else if (wd & kWordMask) {
+          return fail(TTCD_ERR_UNSUPPORTED, "schedule error: mask on a skipped slot (r0=%d n=%d)", r0, n);
         }
-        if (act == kSkip) continue;
-        const bool far = act == kBand2 || act == kFar;
+        // From here on the replay folds what the word says, as the kernel does.
+        if (!w_active) continue;
+        const bool far = (wd & kWordFar) != 0;
         if (sc.dual && !far && student_done)
           return fail(TTCD_ERR_UNSUPPORTED, "schedule error: student keys after emit (r0=%d k=%d)",
                       r0, k);
         if (sc.dual && far && !student_done)
           return fail(TTCD_ERR_UNSUPPORTED, "schedule error: far keys before emit (r0=%d k=%d)",
                       r0, k);
-        const Band band = far ? sc.p2 : sc.p1;
-        const bool full = wave_full(r0, band, j0);
+        const Band band = word_band(sc, wd);
+        const bool full = (wd & kWordMask) == 0;
+        const int wj0 = word_j0(sc, wd);
         for (int i = r0; i < r0 + kWaveRows && i < T; ++i) {
-          for (int j = j0; j < j0 + kBlockN; ++j) {
+          for (int j = wj0; j < wj0 + kBlockN; ++j) {
             if (!(full || visible(i, j, band, T))) continue;
             if (j < 0 || j >= T)
               return fail(TTCD_ERR_UNSUPPORTED, "schedule error: key %d out of range", j);
@@ -952,7 +973,7 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
             cnt[(int64_t)i * T + j] += 1;
           }
         }
-        if (act == kStudentLast) student_done = true;
+        if (wd & kWordLast) student_done = true;
       }
       if (sc.dual && !student_done && sc.p1.lo < sc.p1.hi)
         return fail(TTCD_ERR_UNSUPPORTED, "schedule error: student output never written (r0=%d)",

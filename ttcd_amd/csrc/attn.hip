@@ -239,6 +239,53 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
                : "v"(voff), "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "s"(bs)
                : "memory", "m0");
 }
+// The N loads of one tile by this lane: chunk off[i] of the tile at `base`
+// into LDS bytes lds0 + i * 4096 (i.e. slot (wave + kWaves*i) * 64 + lane of
+// a tile whose wave-0 slot 0 is at lds0 - wave * 1024). One asm block, so the
+// wait state every M0 write needs before the load that uses it is filled by
+// the next LDS address instead of an s_nop.
+template <int N>
+__device__ __forceinline__ void dma_run(const void* base, const uint32_t (&off)[N],
+                                        uint32_t lds0) {
+  static_assert(N == 2 || N == 4, "tile loads per lane");
+  static_assert(kWaves * 1024 == 0x1000, "LDS stride of a lane's loads");
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint64_t bs = (uint64_t)lo | ((uint64_t)hi << 32);
+  const uint32_t l0 = (uint32_t)__builtin_amdgcn_readfirstlane(lds0);
+  uint32_t t;
+  if constexpr (N == 4) {
+    asm volatile(
+        "s_mov_b32 m0, %[l]\n\t"
+        "s_add_u32 %[t], %[l], 0x1000\n\t"
+        "global_load_lds_dwordx4 %[v0], %[b]\n\t"
+        "s_mov_b32 m0, %[t]\n\t"
+        "s_add_u32 %[t], %[l], 0x2000\n\t"
+        "global_load_lds_dwordx4 %[v1], %[b]\n\t"
+        "s_mov_b32 m0, %[t]\n\t"
+        "s_add_u32 %[t], %[l], 0x3000\n\t"
+        "global_load_lds_dwordx4 %[v2], %[b]\n\t"
+        "s_mov_b32 m0, %[t]\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %[v3], %[b]"
+        : [t] "=&s"(t)
+        : [l] "s"(l0), [b] "s"(bs), [v0] "v"(off[0]), [v1] "v"(off[1]), [v2] "v"(off[2]),
+          [v3] "v"(off[3])
+        : "memory", "m0", "scc");
+  } else {
+    asm volatile(
+        "s_mov_b32 m0, %[l]\n\t"
+        "s_add_u32 %[t], %[l], 0x1000\n\t"
+        "global_load_lds_dwordx4 %[v0], %[b]\n\t"
+        "s_mov_b32 m0, %[t]\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %[v1], %[b]"
+        : [t] "=&s"(t)
+        : [l] "s"(l0), [b] "s"(bs), [v0] "v"(off[0]), [v1] "v"(off[1])
+        : "memory", "m0", "scc");
+  }
+}
 #pragma clang diagnostic pop
 
 // Issue the DMA of one K or V tile (rows j0 .. j0+63) into LDS at byte
@@ -366,16 +413,16 @@ __device__ __forceinline__ void score_set(f32x16 (&s)[2], int idx, float v) {
 //            max of slot k (rescaling O^T when it moves) and returns m*c for
 //            its exp2 (+inf for a slot this wave skips); the exp2 / bf16
 //            packing of S(k) is then spread over the remaining MFMAs. K
-//            operand reads run R1 MFMAs ahead. side(i) runs after MFMA i.
+//            operand reads run R1 MFMAs ahead.
 //   phase 2: PV(k) from the V tile at vbase (4*DT MFMAs), with the row sum of
 //            S(k) and then the row max of S(k+1) spread between them and the
 //            V^T operand reads R2 MFMAs ahead.
 // Returns this lane's (unmasked) max of S(k+1), not yet combined across halves.
-template <int D, typename T, typename Settle, typename Side>
+template <int D, typename T, typename Settle>
 __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], f32x16 (&sn)[2],
                                            f32x16 (&o)[Geo<D>::DT], float& l,
                                            const LDS_AS char* kb, const LDS_AS char* vbase,
-                                           Settle&& settle, Side&& side) {
+                                           Settle&& settle) {
   using G = Geo<D>;
   using v8 = typename VecT<T>::v8;
   constexpr int N1 = 2 * G::DK;  // score MFMAs
@@ -424,7 +471,6 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
         }
       }
     }
-    side(i);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -501,8 +547,7 @@ __device__ __forceinline__ void exp_one(const f32x16 (&s)[2], typename VecT<T>::
 // over two slots' MFMAs. Issue order:
 //   phase 1: the scores S(k+1) (2*DK MFMAs), K operand reads R1 ahead, with
 //            the exp2 / packing / row sums of S(k) scores EA .. 31 between
-//            them (scores 0 .. EA-1 ran in the previous slot). side(i) runs
-//            after MFMA i.
+//            them (scores 0 .. EA-1 ran in the previous slot).
 //   check:   rescue(lane sum, mc): one compare and a wave-uniform branch in
 //            the common path. It moves the references of the rows out of
 //            bound, rescales O^T and l, and returns true if S(k) must be
@@ -511,14 +556,14 @@ __device__ __forceinline__ void exp_one(const f32x16 (&s)[2], typename VecT<T>::
 //            S(k+1) scores 0 .. EA-1 into pn, against pre_next() (which masks
 //            S(k+1) if needed and returns its m*c, +inf for a skipped slot).
 // mc and ps0 / ps1 / pe carry the next slot's exp2 state across the call.
-template <int D, typename T, typename PreNext, typename Rescue, typename Side>
+template <int D, typename T, typename PreNext, typename Rescue>
 __device__ __forceinline__ void slot_body_lazy(const Ctx<D, T>& x, f32x16 (&sc)[2],
                                                f32x16 (&sn)[2], typename VecT<T>::v8 (&pc)[4],
                                                typename VecT<T>::v8 (&pn)[4],
                                                f32x16 (&o)[Geo<D>::DT], float& l, float& mc,
                                                float& ps0, float& ps1, float& pe,
                                                const LDS_AS char* kb, const LDS_AS char* vbase,
-                                               PreNext&& pre_next, Rescue&& rescue, Side&& side) {
+                                               PreNext&& pre_next, Rescue&& rescue) {
   using G = Geo<D>;
   using v8 = typename VecT<T>::v8;
   constexpr int N1 = 2 * G::DK;
@@ -553,7 +598,6 @@ __device__ __forceinline__ void slot_body_lazy(const Ctx<D, T>& x, f32x16 (&sc)[
     for (int idx = e0; idx < e1; ++idx) exp_one<T>(sc, pc, idx, x.c, mc, pe, ps0, ps1);
     // keep the sums here, in the MFMA shadow (otherwise they sink to the check)
     asm volatile("" : "+v"(ps0), "+v"(ps1));
-    side(i);
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -581,25 +625,6 @@ __device__ __forceinline__ void slot_body_lazy(const Ctx<D, T>& x, f32x16 (&sc)[
     if (i + R2 < N2) vt[i + R2] = read_vt<D, T>(vb[(i + R2) % G::DT], (i + R2) / G::DT);
     __builtin_amdgcn_sched_barrier(0);
   }
-}
-
-// Per-wave view of one slot of the workgroup's plan.
-struct SlotInfo {
-  int j0;     // first key of the slot's tile
-  int act;    // SlotAction of this wave
-  Band band;  // band the action folds
-  bool mask;  // scores need masking
-};
-
-__device__ __forceinline__ SlotInfo slot_info(const Schedule& sc, const WaveSlots& ws, int n,
-                                              bool repeat, bool valid) {
-  SlotInfo s;
-  s.j0 = sc.tile_start(n);
-  s.act = valid ? ws.act(n, repeat) : (int)kSkip;
-  const bool far = (s.act == kBand2) | (s.act == kFar);
-  s.band = far ? sc.p2 : sc.p1;
-  s.mask = (s.act != kSkip) & ws.mask(n, s.act);
-  return s;
 }
 
 // A wave-uniform 64-bit pointer held in scalar registers.
@@ -714,21 +739,28 @@ void attn_fwd_kernel(AttnArgs a) {
   const WaveSlots wsl(sc, r0);
   const int64_t kst = a.k_st, vst = a.v_st;
   const float rescale_log2 = a.rescale_log2;
-  // DMA of the K (or V) tile of tile index n into the K (V) half of stage s.
-  auto dma_half = [&](bool is_k, int n, int s) __attribute__((always_inline)) {
-    const int j0 = sc.tile_start(n);
+  // Byte address of tile 0's first key (key -kshift) and bytes per key: an
+  // interior tile's address is then one 32 x 32 -> 64-bit product with
+  // (word & ~63) = 64 n (token strides are below 2^25 elements).
+  const uint64_t k_tile0 =
+      reinterpret_cast<uint64_t>(kp) - (uint64_t)((int64_t)sc.kshift * kst * 2);
+  const uint64_t v_tile0 =
+      reinterpret_cast<uint64_t>(vp) - (uint64_t)((int64_t)sc.kshift * vst * 2);
+  const uint32_t k_row_b = (uint32_t)(kst * 2), v_row_b = (uint32_t)(vst * 2);
+  // DMA of the K (or V) tile of the slot with word w into the K (V) half of
+  // stage s; nothing for a word past the last slot.
+  auto dma_half = [&](bool is_k, uint32_t w, int s) __attribute__((always_inline)) {
     const uint32_t dst = lds_base + s * G::STAGE_B + (is_k ? 0 : G::TILE_B);
-    const T* base = is_k ? kp : vp;
-    const int64_t st = is_k ? kst : vst;
-    if (__builtin_expect((j0 >= 0) & (j0 + kBlockN <= T_), 1)) {
-#pragma unroll
-      for (int i = 0; i < G::NDMA; ++i)
-        dma16(base + (int64_t)j0 * st, is_k ? x.ln.k_off[i] : x.ln.v_off[i],
-              dst + (wave + kWaves * i) * 1024);
-    } else if (is_k) {
-      dma_tile<D, T, true>(dst, kp, kst, j0, T_, wave, lane, x.ln.k_off, false);
-    } else {
-      dma_tile<D, T, false>(dst, vp, vst, j0, T_, wave, lane, x.ln.v_off, false);
+    const uint32_t(&off)[G::NDMA] = is_k ? x.ln.k_off : x.ln.v_off;
+    if (__builtin_expect((w & kWordInterior) != 0, 1)) {
+      const uint64_t tile =
+          (is_k ? k_tile0 : v_tile0) + (uint64_t)(w & ~63u) * (is_k ? k_row_b : v_row_b);
+      dma_run<G::NDMA>(reinterpret_cast<const void*>(tile), off, dst + wave * 1024);
+    } else if (w & kWordLoad) {
+      if (is_k)
+        dma_tile<D, T, true>(dst, kp, kst, word_j0(sc, w), T_, wave, lane, off, false);
+      else
+        dma_tile<D, T, false>(dst, vp, vst, word_j0(sc, w), T_, wave, lane, off, false);
     }
   };
 
@@ -749,25 +781,21 @@ void attn_fwd_kernel(AttnArgs a) {
   // K(k+1) and PV reads V(k), so K(k+2) can replace K(k) (read in slot k-1)
   // and V(k+1) can replace V(k-1): both are fetched at the start of slot k
   // and have the whole slot to land.
-  // Prologue: K(0), V(0), K(1) in LDS, scores of slot 0. The walker then
-  // stands at slot 2; (n1, rep1) describes slot 1.
-  SlotWalker walk(sp);
-  walk.n = __builtin_amdgcn_readfirstlane(walk.n);
-#pragma unroll
-  for (int i = 0; i < kWalkDup; ++i) walk.d[i] = __builtin_amdgcn_readfirstlane(walk.d[i]);
-  const int n0 = walk.n;
-  const bool rep0 = walk.rep;
-  if (nslot > 0) {
-    dma_half(true, n0, 0);
-    dma_half(false, n0, 0);
-  }
-  walk.advance();
-  int n1 = walk.n;
-  bool rep1 = walk.rep;
-  if (nslot > 1) dma_half(true, n1, 1);
-  walk.advance();
+  // Slot words (schedule.h: slot_word) of this wave for slots tb .. tb+63,
+  // slot tb + lane in each lane; refreshed every 64 slots and read back one
+  // slot at a time with v_readlane.
+  auto words = [&](int tb) __attribute__((always_inline)) {
+    return slot_word(sc, sp, wsl, nslot, wave_valid, T_, tb + lane);
+  };
+  uint32_t tbl = words(0);
+  // Prologue: K(0), V(0), K(1) in LDS, scores of slot 0. w_cur and w_nxt are
+  // the words of slots 0 and 1.
+  uint32_t w_cur = (uint32_t)__builtin_amdgcn_readlane((int)tbl, 0);
+  uint32_t w_nxt = (uint32_t)__builtin_amdgcn_readlane((int)tbl, 1);
+  dma_half(true, w_cur, 0);
+  dma_half(false, w_cur, 0);
+  dma_half(true, w_nxt, 1);
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  SlotInfo cur = slot_info(sc, wsl, n0, rep0, wave_valid && nslot > 0);
   // Scores of slot 0 and their lane max (unmasked; slot 0's mask and
   // reference max are settled inside the first slot).
   float mx_lane = -INFINITY;
@@ -789,8 +817,9 @@ void attn_fwd_kernel(AttnArgs a) {
   }
   if constexpr (LAZY) {
     // slot 0's first exp2 (the later slots' run under the previous PV)
-    if (__builtin_expect(cur.mask, 0)) mask_band(s0, x.qrow, cur.j0, T_, cur.band, x.half);
-    lz_mc = cur.act != kSkip ? mc_ref : INFINITY;
+    if (__builtin_expect((w_cur & kWordMask) != 0, 0))
+      mask_band(s0, x.qrow, word_j0(sc, w_cur), T_, word_band(sc, w_cur), x.half);
+    lz_mc = (w_cur & kWordActive) ? mc_ref : INFINITY;
 #pragma unroll
     for (int idx = 0; idx < lazy_ea<D>(); ++idx)
       exp_one<T>(s0, pa, idx, x.c, lz_mc, lz_pe, lz_ps0, lz_ps1);
@@ -805,19 +834,19 @@ void attn_fwd_kernel(AttnArgs a) {
   // without register copies.
   auto step = [&](f32x16 (&scur)[2], f32x16 (&snxt)[2], v8 (&pcur)[4], v8 (&pnxt)[4], int k)
                   __attribute__((always_inline)) {
-    const int n2 = walk.n;
-    const bool rep2 = walk.rep;
-    if (k + 2 < nslot) dma_half(true, n2, k & 1);
-    if (k + 1 < nslot) dma_half(false, n1, (k + 1) & 1);
-    SlotInfo nxt;
+    const int k2 = k + 2;
+    if (__builtin_expect((k2 & 63) == 0, 0)) tbl = words(k2);
+    const uint32_t w_k2 = (uint32_t)__builtin_amdgcn_readlane((int)tbl, k2 & 63);
+    dma_half(true, w_k2, k & 1);
+    dma_half(false, w_nxt, (k + 1) & 1);
     // Mask S(k) if needed, then the reference max of slot k (lazy rescale):
     // moved, and O^T / l rescaled, only when some row's max exceeds it by
     // more than 2^rescale_log2 (0: whenever it grows, the reference kernel's
     // exact running max). Returns m*c for the exp2 of slot k.
     auto settle = [&]() __attribute__((always_inline)) {
       float mx = mx_lane;
-      if (__builtin_expect(cur.mask, 0)) {
-        mask_band(scur, x.qrow, cur.j0, T_, cur.band, x.half);
+      if (__builtin_expect((w_cur & kWordMask) != 0, 0)) {
+        mask_band(scur, x.qrow, word_j0(sc, w_cur), T_, word_band(sc, w_cur), x.half);
         float a0 = -INFINITY, a1 = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -827,7 +856,7 @@ void attn_fwd_kernel(AttnArgs a) {
         mx = fmaxf(a0, a1);
       }
       mx = xhalf_max(mx);
-      const bool active = cur.act != kSkip;
+      const bool active = (w_cur & kWordActive) != 0;
       const float m_new = active ? fmaxf(m, mx) : m;
       const bool grow = (m_new > m) & ((m == -INFINITY) | ((m_new - m) * x.c > rescale_log2));
       if (__builtin_expect(__any(grow) != 0, 0)) {
@@ -844,24 +873,22 @@ void attn_fwd_kernel(AttnArgs a) {
       }
       return active ? ((m == -INFINITY) ? 0.f : m * x.c) : INFINITY;
     };
-    auto side = [&](int i) __attribute__((always_inline)) {
-      if (i == 2) nxt = slot_info(sc, wsl, n1, rep1, wave_valid & (k + 1 < nslot));
-    };
     const LDS_AS char* kb = x.lds + ((k + 1) & 1) * G::STAGE_B;
     const LDS_AS char* vbase = x.lds + (k & 1) * G::STAGE_B + G::TILE_B;
     if constexpr (LAZY) {
       // Mask S(k+1) if needed; m*c for its exp2 (+inf for a slot this wave
       // skips).
       auto pre_next = [&]() __attribute__((always_inline)) {
-        if (__builtin_expect(nxt.mask, 0)) mask_band(snxt, x.qrow, nxt.j0, T_, nxt.band, x.half);
-        return nxt.act != kSkip ? mc_ref : INFINITY;
+        if (__builtin_expect((w_nxt & kWordMask) != 0, 0))
+          mask_band(snxt, x.qrow, word_j0(sc, w_nxt), T_, word_band(sc, w_nxt), x.half);
+        return (w_nxt & kWordActive) ? mc_ref : INFINITY;
       };
       // A row is out of bound when either half's sum t exceeds 2^rescale_log2
       // or it has no reference yet. Such rows move their reference to their
       // running max (O^T and l rescaled); the others keep theirs (alpha = 1,
       // the same p), so a row's arithmetic depends on its own scores alone.
       auto rescue = [&](float t, float& mc) __attribute__((always_inline)) {
-        const bool active = cur.act != kSkip;
+        const bool active = (w_cur & kWordActive) != 0;
         const bool out = active & (!(t <= bound) | (m == -INFINITY));
         if (__builtin_expect(__any(out) == 0, 1)) return false;
         float a0 = -INFINITY, a1 = -INFINITY;
@@ -885,20 +912,18 @@ void attn_fwd_kernel(AttnArgs a) {
         return true;
       };
       slot_body_lazy<D, T>(x, scur, snxt, pcur, pnxt, o, l, lz_mc, lz_ps0, lz_ps1, lz_pe, kb,
-                           vbase, pre_next, rescue, side);
+                           vbase, pre_next, rescue);
     } else {
-      mx_lane = slot_body<D, T>(x, scur, snxt, o, l, kb, vbase, settle, side);
+      mx_lane = slot_body<D, T>(x, scur, snxt, o, l, kb, vbase, settle);
     }
-    if (DUAL && cur.act == kStudentLast) {
+    if (DUAL && (w_cur & kWordLast)) {
       T* os = static_cast<T*>(a.o_s) + o_base;
       float* lse_s = a.lse_s ? a.lse_s + lse_base : nullptr;
       emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, q_off, lane);
       emitted_s = true;
     }
-    cur = nxt;
-    walk.advance();
-    n1 = n2;
-    rep1 = rep2;
+    w_cur = w_nxt;
+    w_nxt = w_k2;
     // K(k+2) and V(k+1), fetched at the start of this slot, are read in the next.
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   };

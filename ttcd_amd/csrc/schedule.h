@@ -191,35 +191,6 @@ TTCD_HD SlotPlan make_slot_plan(const Schedule& sc, R0 r0_of_wave, int n_hi, int
   return sp;
 }
 
-// Distinct repeated tiles a plan can hold: at most one per wave (the two
-// waves of an aligned 64-row pair share theirs only when ws mod 64 < 32).
-constexpr int kWalkDup = kMaxDup;
-
-// Walks the slots of a plan in order with O(1) work per slot: the current
-// tile, whether the slot repeats the previous tile, and the remaining
-// repeated tiles (descending; consumed from the front).
-struct SlotWalker {
-  int n;
-  bool rep;
-  int d[kWalkDup];
-
-  TTCD_HD explicit SlotWalker(const SlotPlan& sp) : n(sp.n_hi), rep(false) {
-#pragma unroll
-    for (int i = 0; i < kWalkDup; ++i) d[i] = sp.dup[i];
-  }
-  TTCD_HD void advance() {
-    if (!rep && n == d[0]) {
-      rep = true;
-#pragma unroll
-      for (int i = 0; i + 1 < kWalkDup; ++i) d[i] = d[i + 1];
-      d[kWalkDup - 1] = kNoTile;
-    } else {
-      rep = false;
-      n -= 1;
-    }
-  }
-};
-
 // What a wave folds in a slot: nothing, one band (mask chosen by wave_full),
 // the student part of its mixed tile (then writes the student output) or the
 // far part (repeat slot).
@@ -290,6 +261,48 @@ struct WaveSlots {
     return !((n >= fa) & (n <= fz));
   }
 };
+
+// Slot words: everything the slot loop needs about slot k for one wave, in
+// one 32-bit word. The kernel computes 64 consecutive slots at once (slot
+// base + lane in each lane) and reads one word per slot back with
+// v_readlane, so a slot costs a few scalar bit tests instead of evaluating
+// the plan, the actions and the load bounds. Bits 0-5 are flags; bits 6+
+// hold the tile index, so (word & ~63) is the tile's first key + kshift.
+enum SlotWordBits : uint32_t {
+  kWordLoad = 1u,      // slot exists: its K and V tiles are loaded
+  kWordInterior = 2u,  // tile keys all inside [0, T): unclamped loads
+  kWordActive = 4u,    // this wave folds keys (action != kSkip)
+  kWordFar = 8u,       // ... of phase 2 (kBand2 or kFar), else of phase 1
+  kWordLast = 16u,     // ... and it is kStudentLast (student output follows)
+  kWordMask = 32u,     // ... and the scores need masking
+};
+constexpr int kWordTileShift = 6;
+static_assert((1 << kWordTileShift) == kBlockN, "word & ~63 is the tile's key offset");
+
+// Word of slot k of plan sp (nslot slots) for the wave described by ws
+// (wave_valid false: a wave without rows, which only loads), keys [0, T).
+TTCD_HD uint32_t slot_word(const Schedule& sc, const SlotPlan& sp, const WaveSlots& ws,
+                           int nslot, bool wave_valid, int T, int k) {
+  bool repeat;
+  int n = sp.tile(k, &repeat);
+  const bool load = (k >= 0) & (k < nslot);
+  n = load ? n : 0;
+  const int j0 = sc.tile_start(n);
+  const int act = (load & wave_valid) ? ws.act(n, repeat) : (int)kSkip;
+  const bool far = (act == kBand2) | (act == kFar);
+  uint32_t w = (uint32_t)n << kWordTileShift;
+  w |= load ? kWordLoad : 0u;
+  w |= (load & (j0 >= 0) & (j0 + kBlockN <= T)) ? kWordInterior : 0u;
+  w |= act != kSkip ? kWordActive : 0u;
+  w |= far ? kWordFar : 0u;
+  w |= act == kStudentLast ? kWordLast : 0u;
+  w |= (act != kSkip && ws.mask(n, act)) ? kWordMask : 0u;
+  return w;
+}
+
+TTCD_HD int word_tile(uint32_t w) { return (int)(w >> kWordTileShift); }
+TTCD_HD int word_j0(const Schedule& sc, uint32_t w) { return (int)(w & ~63u) - sc.kshift; }
+TTCD_HD Band word_band(const Schedule& sc, uint32_t w) { return (w & kWordFar) ? sc.p2 : sc.p1; }
 
 // Query tokens swept by one workgroup (see Geometry; the same for every GQA group size).
 TTCD_HD int wg_span_tokens(int gqa_group) {
