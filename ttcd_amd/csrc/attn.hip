@@ -433,17 +433,14 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
   constexpr int H2 = N2 / 2;     // PV MFMAs carrying sums (the rest carry maxima)
   constexpr int A2 = 32 / H2;    // values summed / maxed per PV MFMA
 
-  // Lane addresses, opaque per slot so the compiler forms the derived
-  // addresses here instead of holding them all in registers.
+  // The K lane address is opaque per slot, so its eight per-k-step XORs are
+  // formed here instead of held in registers (the V^T addresses' per-k-step
+  // parts are immediate offsets and need no such fence).
   uint32_t xk = x.ln.xk;
   asm volatile("" : "+v"(xk));
   const LDS_AS char* vb[G::DT];
 #pragma unroll
-  for (int dt = 0; dt < G::DT; ++dt) {
-    uint32_t a = x.ln.vb[dt];
-    asm volatile("" : "+v"(a));
-    vb[dt] = vbase + a;
-  }
+  for (int dt = 0; dt < G::DT; ++dt) vb[dt] = vbase + x.ln.vb[dt];
 
   // phase 1
   v8 ka[N1];
@@ -573,15 +570,15 @@ __device__ __forceinline__ void slot_body_lazy(const Ctx<D, T>& x, f32x16 (&sc)[
   constexpr int EA = lazy_ea<D>();
   static_assert(EA >= 0 && EA <= 32, "scores per phase");
 
+  // The K lane address is opaque per slot, so its eight per-k-step XORs are
+  // formed here instead of held in registers. The V^T addresses need no such
+  // fence (their per-k-step parts are immediate offsets); one costs four
+  // register copies per slot and, at this register budget, a spill.
   uint32_t xk = x.ln.xk;
   asm volatile("" : "+v"(xk));
   const LDS_AS char* vb[G::DT];
 #pragma unroll
-  for (int dt = 0; dt < G::DT; ++dt) {
-    uint32_t a = x.ln.vb[dt];
-    asm volatile("" : "+v"(a));
-    vb[dt] = vbase + a;
-  }
+  for (int dt = 0; dt < G::DT; ++dt) vb[dt] = vbase + x.ln.vb[dt];
 
   // phase 1
   v8 ka[N1];
