@@ -412,8 +412,9 @@ ttcd_status ttcd_ttt_scan_fwd(const void* dw, const void* w_cur, float lr, void*
  * window_s <= i - j < window_t). Used by tests to prove every in-band pair
  * is visited exactly once. Set dual = 0 for the single-band schedule, in
  * which case window_s = band_lo and window_t = band_hi. gqa_group is the
- * query-head group size Hq/Hkv (the current workgroup geometry, 128 tokens
- * of one head, does not depend on it). The pairs are counted from the
+ * query-head group size Hq/Hkv, which sets the workgroup geometry: 4
+ * wavefronts of 16 rows (64 tokens) for an even group, of 32 rows (128
+ * tokens) otherwise. The pairs are counted from the
  * per-slot words the kernel decodes (tile, action, band, mask, load bounds),
  * each first checked against the plan and the per-tile predicates.
  */

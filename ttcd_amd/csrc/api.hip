@@ -188,7 +188,7 @@ ttcd_status ttcd_dual_window_attn_kv_fwd(const void* q, const void* k, const voi
   a.lse_t = lse_t;
   a.lse_s = lse_s;
   a.rescale_log2 = rescale_log2;
-  a.sched = ttcd::make_dual_schedule(Tk, window_s, window_t);
+  a.sched = ttcd::make_dual_schedule(Tk, window_s, window_t, ttcd::wave_rows(a.G));
   return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
                   "dual-window attention launch");
 }
@@ -226,7 +226,7 @@ ttcd_status ttcd_band_attn_kv_fwd(const void* q, const void* k, const void* v, v
   a.o_t = o;
   a.lse_t = lse;
   a.rescale_log2 = rescale_log2;
-  a.sched = ttcd::make_band_schedule(Tk, band_lo, band_hi);
+  a.sched = ttcd::make_band_schedule(Tk, band_lo, band_hi, ttcd::wave_rows(a.G));
   return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
                   "band attention launch");
 }
@@ -304,7 +304,7 @@ ttcd_status ttcd_dual_window_attn_varlen_fwd(const void* q, const void* k, const
   a.lse_s = lse_s;
   a.win_a = window_s;
   a.win_b = window_t;
-  a.sched = ttcd::make_dual_schedule(max_seqlen, window_s, window_t);
+  a.sched = ttcd::make_dual_schedule(max_seqlen, window_s, window_t, ttcd::wave_rows(a.G));
   return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
                   "varlen dual-window attention launch");
 }
@@ -328,7 +328,7 @@ ttcd_status ttcd_band_attn_varlen_fwd(const void* q, const void* k, const void* 
   a.lse_t = lse;
   a.win_a = band_lo;
   a.win_b = band_hi;
-  a.sched = ttcd::make_band_schedule(max_seqlen, band_lo, band_hi);
+  a.sched = ttcd::make_band_schedule(max_seqlen, band_lo, band_hi, ttcd::wave_rows(a.G));
   return from_hip(ttcd::launch_attn(a, D, elem(dtype), static_cast<hipStream_t>(stream)),
                   "varlen band attention launch");
 }
@@ -890,16 +890,16 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
     if (window_t < 0) window_t = T;
     if (window_s < 1 || window_s > window_t)
       return fail(TTCD_ERR_INVALID_ARGUMENT, "need 1 <= window_s <= window_t");
-    sc = make_dual_schedule(T, window_s, window_t);
+    sc = make_dual_schedule(T, window_s, window_t, wave_rows(gqa_group));
   } else {
     if (window_s < 0 || window_t <= window_s)
       return fail(TTCD_ERR_INVALID_ARGUMENT, "need 0 <= band_lo < band_hi");
-    sc = make_band_schedule(T, window_s, window_t);
+    sc = make_band_schedule(T, window_s, window_t, wave_rows(gqa_group));
   }
-  // Workgroup geometry as launched (attn.hip): 4 waves over 128 consecutive
-  // tokens of one head, wave w owning rows r0 = t0 + 32*w (gqa_group does not
-  // change it).
-  (void)gqa_group;
+  // Workgroup geometry as launched (attn.hip): 4 waves over 4R consecutive
+  // tokens, wave w owning rows r0 = t0 + R*w (R = 16 for an even gqa_group,
+  // else 32).
+  const int R = sc.rows;
   const int span = wg_span_tokens(gqa_group);
   const int nwg = (T + span - 1) / span;
   for (int qb = 0; qb < nwg; ++qb) {
@@ -907,11 +907,11 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
     const int t_last = (t0 + span < T ? t0 + span : T) - 1;
     int n_hi, n_lo;
     if (!sc.wg_range(t0, t_last, &n_hi, &n_lo)) continue;
-    auto r0_of_wave = [&](int wv) { return t0 + wv * kWaveRows; };
+    auto r0_of_wave = [&](int wv) { return t0 + wv * R; };
     const SlotPlan sp = make_slot_plan(sc, r0_of_wave, n_hi, n_lo);
     const int nslot = sp.slots();
-    for (int w = 0; w < span / kWaveRows; ++w) {
-      const int r0 = t0 + w * kWaveRows;
+    for (int w = 0; w < kWaves; ++w) {
+      const int r0 = t0 + w * R;
       if (r0 >= T) continue;
       bool student_done = false;
       const WaveSlots ws(sc, r0);  // the kernel's closed form
@@ -946,7 +946,7 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
           const Band wb = word_band(sc, wd);
           if (wb.lo != b.lo || wb.hi != b.hi)
             return fail(TTCD_ERR_UNSUPPORTED, "schedule error: slot word band (r0=%d n=%d)", r0, n);
-          const bool need_mask = !wave_full(r0, b, j0);
+          const bool need_mask = !wave_full(r0, R, b, j0);
           if (ws.mask(n, act) != need_mask || ((wd & kWordMask) != 0) != need_mask)
             return fail(TTCD_ERR_UNSUPPORTED, "schedule error: closed-form mask (r0=%d n=%d)", r0, n);
         } else if (wd & kWordMask) {
@@ -964,7 +964,7 @@ ttcd_status ttcd_attn_schedule_coverage(int T, int dual, int window_s, int windo
         const Band band = word_band(sc, wd);
         const bool full = (wd & kWordMask) == 0;
         const int wj0 = word_j0(sc, wd);
-        for (int i = r0; i < r0 + kWaveRows && i < T; ++i) {
+        for (int i = r0; i < r0 + R && i < T; ++i) {
           for (int j = wj0; j < wj0 + kBlockN; ++j) {
             if (!(full || visible(i, j, band, T))) continue;
             if (j < 0 || j >= T)

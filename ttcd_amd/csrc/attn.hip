@@ -6,11 +6,16 @@
 // calls of the LSE variant (profiling/lse_dual_attn.py:22-29, :143-149).
 //
 // Mapping onto CDNA4
-//   * One workgroup = 4 wavefronts: 128 query tokens of one query head, 32
-//     rows per wavefront. D = 128: two workgroups per CU (64 KiB of LDS
-//     each, <= 256 VGPRs); D = 64: three (32 KiB each, <= 168 VGPRs). The two
-//     or three wavefronts sharing a SIMD come from different workgroups, so
-//     one's barrier and DMA time is filled by another's MFMAs.
+//   * One workgroup = 4 wavefronts of 32 query columns each: 32 rows of one
+//     query head (128 tokens per workgroup), or, when the GQA group size is
+//     even, 16 rows of each of two query heads that share the K/V head (64
+//     tokens per workgroup; every MFMA operand is shared, and the workgroup's
+//     narrower row span sweeps fewer partly-used tiles: one repeated mixed
+//     tile instead of two, no skipped edge tiles). D = 128: two workgroups
+//     per CU (64 KiB of LDS each, <= 256 VGPRs); D = 64: three (32 KiB each,
+//     <= 168 VGPRs). The two or three wavefronts sharing a SIMD come from
+//     different workgroups, so one's barrier and DMA time is filled by
+//     another's MFMAs.
 //   * K and V tiles (64 keys) go global -> LDS by DMA
 //     (global_load_lds_dwordx4, no registers) in a two-stage split ring: slot
 //     k reads K(k+1) and V(k), so K(k+2) and V(k+1) are fetched at its start
@@ -656,18 +661,25 @@ void attn_fwd_kernel(AttnArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // Workgroup -> (b, kv head, query block [heaviest first], head in group),
+  // Wavefront geometry: R query rows per wavefront, 32 of one head or (hpw =
+  // 2, even GQA group) 16 of each of two heads of the group; score column
+  // n = lane % 32 is row n % R of head h + n / R.
+  const int R = a.sched.rows;
+  const int hpw = kWaveRows / R;
+  const int span = kWaves * R;
+  // Workgroup -> (b, kv head, query block [heaviest first], head group),
   // XCD-remapped: each XCD sweeps a contiguous run, so the query heads
   // sharing a K/V head and neighbouring query blocks share its L2.
   int rest = xcd_remap(__builtin_amdgcn_workgroup_id_x(), a.nwg);
-  const int g = rest % a.G;
-  rest /= a.G;
+  const int ngrp = a.G / hpw;
+  const int g = rest % ngrp;
+  rest /= ngrp;
   const int qb = a.qb0 + (a.nqb - 1 - rest % a.nqb);
   rest /= a.nqb;
   const int hk = rest % a.Hkv;
   const int b = rest / a.Hkv;
-  const int h = hk * a.G + g;
-  const int t0 = qb * kBlockM;
+  const int h = hk * a.G + g * hpw + (hpw == 2 ? (lane >> 4) & 1 : 0);  // this lane's head
+  const int t0 = qb * span;
 
   // Packed sequences: sequence b is rows row0 .. row0 + T_ - 1 of every
   // tensor, with its own schedule. The bounds are clamped to the packed
@@ -682,18 +694,18 @@ void attn_fwd_kernel(AttnArgs a) {
     const int c1 = __builtin_amdgcn_readfirstlane(a.cu_seqlens[b + 1]);
     const int s0 = min(max(c0, 0), a.total);
     const int s1 = min(max(c1, s0), a.total);
-    T_ = min(s1 - s0, a.nqb * kBlockM);
+    T_ = min(s1 - s0, a.nqb * span);
     row0 = s0;
-    sc = sc.dual ? make_dual_schedule(T_, a.win_a, a.win_b)
-                 : make_band_schedule(T_, a.win_a, a.win_b);
+    sc = sc.dual ? make_dual_schedule(T_, a.win_a, a.win_b, R)
+                 : make_band_schedule(T_, a.win_a, a.win_b, R);
     if (t0 >= T_) return;
   }
-  const int r0 = __builtin_amdgcn_readfirstlane(t0 + wave * kWaveRows);
-  const int t_last = min(t0 + kBlockM, T_) - 1;
+  const int r0 = __builtin_amdgcn_readfirstlane(t0 + wave * R);
+  const int t_last = min(t0 + span, T_) - 1;
   const int q_off = a.q_off;
   // a wave with no row in [q_off, T) computes nothing (it still takes part
   // in the workgroup's loads and barriers)
-  const bool wave_valid = (r0 < T_) & (r0 + kWaveRows > q_off);
+  const bool wave_valid = (r0 < T_) & (r0 + R > q_off);
 
   const T* qp = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh + row0 * a.q_st;
   const T* kp =
@@ -708,7 +720,7 @@ void attn_fwd_kernel(AttnArgs a) {
   x.lds = (LDS_AS char*)smem_raw;
   const uint32_t lds_base = (uint32_t)(uintptr_t)x.lds;
   x.c = a.c;
-  x.qrow = r0 + (lane & 31);
+  x.qrow = r0 + (lane & (R - 1));
   x.half = lane >> 5;
   x.T_ = T_;
   x.ln = make_lane<D>(a.k_st, a.v_st, wave, lane);
@@ -729,7 +741,7 @@ void attn_fwd_kernel(AttnArgs a) {
   }
   const int count = n_hi - n_lo + 1;
   const SlotPlan sp = make_slot_plan(
-      sc, [&](int wv) { return t0 + wv * kWaveRows; }, n_hi, n_lo);
+      sc, [&](int wv) { return t0 + wv * R; }, n_hi, n_lo);
   // The plan is workgroup-uniform; keep it in scalar registers.
   const int nslot = __builtin_amdgcn_readfirstlane(count > 0 ? sp.slots() : 0);
 
@@ -945,7 +957,7 @@ void attn_fwd_kernel(AttnArgs a) {
 template <int D, typename T, bool DUAL>
 hipError_t launch_typed(const AttnArgs& a, hipStream_t stream) {
   AttnArgs args = a;
-  args.nwg = a.B * a.Hq * a.nqb;
+  args.nwg = a.B * (a.Hq / (kWaveRows / a.sched.rows)) * a.nqb;
   // The sum-triggered lazy slot needs a second P^T buffer, which D = 64 has
   // no registers for at three waves per SIMD; D = 64 and the exact mode take
   // the max-first slot.

@@ -27,8 +27,8 @@ struct AttnArgs {
   int B, T, Hq, Hkv, G;  // T: keys (Tk); query rows are absolute positions q_off..T-1
   int q_off;      // Tk - Tq: absolute position of query row 0 (flash-attention's
                   // bottom-right alignment; 0 when Tq == Tk)
-  int qb0;        // first query tile launched: q_off / kBlockM
-  int nqb;        // query tiles of kBlockM tokens per (b, h) launched
+  int qb0;        // first query tile launched: q_off / (4 * sched.rows)
+  int nqb;        // query tiles of 4 * sched.rows tokens per (b, head group) launched
   int nwg;        // workgroups launched (set by the launcher)
   float c;        // sm_scale * log2(e)
   float rescale_log2;  // lazy online softmax: the reference max moves when a row max

@@ -5,13 +5,15 @@
 // the exact iteration logic the GPU runs: every (query, key) pair inside a
 // window is folded into that window's output exactly once.
 //
-// Geometry. A workgroup has 4 wavefronts; each wavefront owns 32 consecutive
-// query rows (r0..r0+31) of one query head, so a workgroup owns kBlockM = 128
-// tokens of one head. Keys are swept in tiles of kBlockN = 64, tile n
-// covering keys [64n - kshift, 64n - kshift + 63], from the tile holding the
-// workgroup's last diagonal downward (the same backward-from-diagonal order
-// as profiling/fused_dual_attn.py:91,119,151,176,191); every wave of the
-// workgroup steps through the same tiles.
+// Geometry. A workgroup has 4 wavefronts; each wavefront owns R consecutive
+// query rows (r0..r0+R-1), R = Schedule::rows: 32 rows of one query head, or,
+// for an even GQA group, 16 rows of each of two query heads of the group (the
+// 32 columns of one score MFMA; both heads read the same K/V, so every MFMA
+// operand is shared). A workgroup owns 4R tokens. Keys are swept in tiles of
+// kBlockN = 64, tile n covering keys [64n - kshift, 64n - kshift + 63], from
+// the tile holding the workgroup's last diagonal downward (the same
+// backward-from-diagonal order as profiling/fused_dual_attn.py:91,119,151,
+// 176,191); every wave of the workgroup steps through the same tiles.
 //
 // Phases. A band {lo, hi} selects keys with lo <= i - j < hi. The dual kernel
 // runs phase 1 = student band {0, ws} and then phase 2 = far band {ws, wt}
@@ -23,12 +25,15 @@
 // output accumulator in registers.
 //
 // The single-accumulator order needs every wave's "mixed" keys (keys that
-// are student-visible for some of its rows and far for others: the 31 keys
-// [r0-ws+1, r0+31-ws]) to sit in one tile, so that all phase-1 tiles of a
-// wave precede all of its phase-2-only tiles. With r0 a multiple of 32 this
-// holds iff tile starts are congruent to (1 - ws) or (-ws) modulo 32, hence
-// kshift = ws mod 32 for the dual kernel (0 for single-band calls). It also
-// makes the two waves of each aligned 64-row pair share their mixed tile.
+// are student-visible for some of its rows and far for others: the R-1 keys
+// [r0-ws+1, r0+R-1-ws]) to sit in one tile, so that all phase-1 tiles of a
+// wave precede all of its phase-2-only tiles. With r0 a multiple of R this
+// holds iff tile starts are congruent to (1 - ws) or (-ws) modulo R, so
+// kshift = ws mod 32 serves both geometries (0 for single-band calls). It
+// also makes the waves of each aligned 64-row run share their mixed tile:
+// one repeated tile per 16-row-wave workgroup (two for 32-row waves) when
+// ws mod 64 < 32. The tile boundaries, and with them every row's order of
+// accumulation, are the same in both geometries.
 #pragma once
 
 #include <stdint.h>
@@ -42,9 +47,9 @@
 namespace ttcd {
 
 constexpr int kBlockN = 64;    // keys per K/V tile
-constexpr int kWaveRows = 32;  // query rows per wavefront
+constexpr int kWaveRows = 32;  // query columns per wavefront (score MFMA columns)
 constexpr int kWaves = 4;      // wavefronts per workgroup
-constexpr int kBlockM = kWaveRows * kWaves;  // query tokens per workgroup
+constexpr int kBlockM = kWaveRows * kWaves;  // query tokens per workgroup, one head per wave
 
 struct Band {
   int lo;  // inclusive lower bound of i - j
@@ -60,6 +65,7 @@ struct Schedule {
   Band p1;     // phase-1 band
   Band p2;     // phase-2 band (dual only; empty when lo == hi)
   int kshift;  // tile n starts at key 64n - kshift
+  int rows;    // query rows (tokens) per wavefront: 32, or 16 of each of two heads
 
   TTCD_HD int tile_of(int j) const { return floordiv(j + kshift, kBlockN); }
   TTCD_HD int tile_start(int n) const { return n * kBlockN - kshift; }
@@ -78,16 +84,14 @@ struct Schedule {
   }
 };
 
-// Does tile [j0, j0+63] hold a key of band b for some row of the wave r0..r0+31?
-TTCD_HD bool wave_touches(int r0, Band b, int j0) {
-  return b.lo < b.hi && j0 + kBlockN - 1 >= r0 - b.hi + 1 &&
-         j0 <= r0 + kWaveRows - 1 - b.lo;
+// Does tile [j0, j0+63] hold a key of band b for some row of the wave r0..r0+R-1?
+TTCD_HD bool wave_touches(int r0, int R, Band b, int j0) {
+  return b.lo < b.hi && j0 + kBlockN - 1 >= r0 - b.hi + 1 && j0 <= r0 + R - 1 - b.lo;
 }
 
 // Is every (row, key) pair of the tile inside band b (no mask needed)?
-TTCD_HD bool wave_full(int r0, Band b, int j0) {
-  return j0 >= 0 && r0 - (j0 + kBlockN - 1) >= b.lo &&
-         r0 + kWaveRows - 1 - j0 < b.hi;
+TTCD_HD bool wave_full(int r0, int R, Band b, int j0) {
+  return j0 >= 0 && r0 - (j0 + kBlockN - 1) >= b.lo && r0 + R - 1 - j0 < b.hi;
 }
 
 // Is this the wave's last tile of band b in the backward sweep?
@@ -147,7 +151,8 @@ TTCD_HD int wave_mixed_tile(const Schedule& sc, int r0) {
   if (lowest < 0) lowest = 0;
   const int n = sc.tile_of(lowest);
   const int j0 = sc.tile_start(n);
-  return (wave_touches(r0, sc.p1, j0) && wave_touches(r0, sc.p2, j0)) ? n : kNoTile;
+  return (wave_touches(r0, sc.rows, sc.p1, j0) && wave_touches(r0, sc.rows, sc.p2, j0)) ? n
+                                                                                   : kNoTile;
 }
 
 // Slot plan of a workgroup whose wave w starts at row r0_of_wave(w) (rows >= T
@@ -197,8 +202,8 @@ TTCD_HD SlotPlan make_slot_plan(const Schedule& sc, R0 r0_of_wave, int n_hi, int
 enum SlotAction { kSkip = 0, kBand1 = 1, kBand2 = 2, kStudentLast = 3, kFar = 4 };
 
 TTCD_HD int slot_action(const Schedule& sc, int r0, int j0, bool repeat) {
-  const bool in1 = wave_touches(r0, sc.p1, j0);
-  const bool in2 = sc.dual && wave_touches(r0, sc.p2, j0);
+  const bool in1 = wave_touches(r0, sc.rows, sc.p1, j0);
+  const bool in2 = sc.dual && wave_touches(r0, sc.rows, sc.p2, j0);
   if (repeat) return (in1 && in2) ? kFar : kSkip;
   if (in1 && (in2 || (sc.dual && wave_last(r0, sc.p1, j0)))) return kStudentLast;
   return in1 ? kBand1 : (in2 ? kBand2 : kSkip);
@@ -221,7 +226,7 @@ struct WaveSlots {
     auto range = [&](Band b, int* a, int* z) {
       if (b.lo < b.hi) {
         *a = sc.tile_of(r0 - b.hi + 1);
-        *z = sc.tile_of(r0 + kWaveRows - 1 - b.lo);
+        *z = sc.tile_of(r0 + sc.rows - 1 - b.lo);
       } else {
         *a = big;
         *z = -big;
@@ -238,7 +243,7 @@ struct WaveSlots {
     nl = sc.tile_of(lowest > 0 ? lowest : 0);
     const int nz = sc.kshift > 0 ? 1 : 0;  // first tile with j0 >= 0
     auto full = [&](Band b, int* a, int* z) {
-      const int lo_t = sc.tile_of(r0 + kWaveRows + kBlockN - 1 - b.hi);  // j0 > r0 + 31 - hi
+      const int lo_t = sc.tile_of(r0 + sc.rows + kBlockN - 1 - b.hi);  // j0 > r0 + R-1 - hi
       *a = lo_t > nz ? lo_t : nz;
       *z = sc.tile_of(r0 - (kBlockN - 1) - b.lo);                      // j0 <= r0 - 63 - lo
     };
@@ -304,14 +309,21 @@ TTCD_HD int word_tile(uint32_t w) { return (int)(w >> kWordTileShift); }
 TTCD_HD int word_j0(const Schedule& sc, uint32_t w) { return (int)(w & ~63u) - sc.kshift; }
 TTCD_HD Band word_band(const Schedule& sc, uint32_t w) { return (w & kWordFar) ? sc.p2 : sc.p1; }
 
-// Query tokens swept by one workgroup (see Geometry; the same for every GQA group size).
-TTCD_HD int wg_span_tokens(int gqa_group) {
-  (void)gqa_group;
-  return kBlockM;
+// Query rows per wavefront for a GQA group size (see Geometry): 16 rows of
+// each of two heads for an even group, else 32 rows of one head.
+#ifndef TTCD_PAIR_WAVES
+#define TTCD_PAIR_WAVES 1
+#endif
+TTCD_HD int wave_rows(int gqa_group) {
+  return (TTCD_PAIR_WAVES && gqa_group % 2 == 0) ? kWaveRows / 2 : kWaveRows;
 }
 
-// Schedules built by the C ABI entry points (windows already validated).
-TTCD_HD Schedule make_dual_schedule(int T, int ws, int wt) {
+// Query tokens swept by one workgroup.
+TTCD_HD int wg_span_tokens(int gqa_group) { return kWaves * wave_rows(gqa_group); }
+
+// Schedules built by the C ABI entry points (windows already validated), for
+// wavefronts of `rows` query rows.
+TTCD_HD Schedule make_dual_schedule(int T, int ws, int wt, int rows) {
   if (wt > T) wt = T;
   if (ws > wt) ws = wt;
   Schedule s;
@@ -322,10 +334,11 @@ TTCD_HD Schedule make_dual_schedule(int T, int ws, int wt) {
   s.p2.lo = ws;
   s.p2.hi = wt;
   s.kshift = ws % kWaveRows;
+  s.rows = rows;
   return s;
 }
 
-TTCD_HD Schedule make_band_schedule(int T, int lo, int hi) {
+TTCD_HD Schedule make_band_schedule(int T, int lo, int hi, int rows) {
   if (hi > T) hi = T;
   if (lo > hi) lo = hi;
   Schedule s;
@@ -336,6 +349,7 @@ TTCD_HD Schedule make_band_schedule(int T, int lo, int hi) {
   s.p2.lo = hi;
   s.p2.hi = hi;
   s.kshift = 0;
+  s.rows = rows;
   return s;
 }
 
