@@ -41,7 +41,8 @@
 //     is needed before the exp2, so the PV MFMAs of slot k run under the
 //     first half of S(k+1)'s exp2 instead (slot_body_lazy).
 //   * Workgroups are remapped so each XCD (own L2) sweeps a contiguous run of
-//     (b, kv head, query block, head in group); heaviest query blocks first.
+//     (b, kv head, query block, head or head pair in group); heaviest query
+//     blocks first.
 //   * Packed sequences (cu_seqlens): each workgroup builds its sequence's
 //     schedule from the sequence length, with every bound clamped to the
 //     packed tensors.
@@ -678,7 +679,10 @@ void attn_fwd_kernel(AttnArgs a) {
   rest /= a.nqb;
   const int hk = rest % a.Hkv;
   const int b = rest / a.Hkv;
-  const int h = hk * a.G + g * hpw + (hpw == 2 ? (lane >> 4) & 1 : 0);  // this lane's head
+  const int h = hk * a.G + g * hpw;  // the wavefront's first query head
+  // this lane's head is h + dh (kept out of the uniform bases below, so they
+  // stay in scalar registers through the sweep)
+  const bool dh = hpw == 2 && ((lane >> 4) & 1) != 0;
   const int t0 = qb * span;
 
   // Packed sequences: sequence b is rows row0 .. row0 + T_ - 1 of every
@@ -707,14 +711,18 @@ void attn_fwd_kernel(AttnArgs a) {
   // in the workgroup's loads and barriers)
   const bool wave_valid = (r0 < T_) & (r0 + R > q_off);
 
-  const T* qp = static_cast<const T*>(a.q) + b * a.q_sb + h * a.q_sh + row0 * a.q_st;
+  const T* qp =
+      static_cast<const T*>(a.q) + b * a.q_sb + (h + dh) * a.q_sh + row0 * a.q_st;
   const T* kp =
       uniform_ptr(static_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh + row0 * a.k_st);
   const T* vp =
       uniform_ptr(static_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh + row0 * a.v_st);
-  // first output row / LSE entry of this (b, h)
+  // first output row / LSE entry of this (b, h); the lane's own head adds
+  // o_dh / lse_dh
   const int64_t o_base = b * a.o_sb + h * a.o_sh + row0 * a.o_st;
   const int64_t lse_base = b * a.lse_sb + h * a.lse_sh + row0;
+  auto o_dh = [&]() __attribute__((always_inline)) { return dh ? a.o_sh : (int64_t)0; };
+  auto lse_dh = [&]() __attribute__((always_inline)) { return dh ? a.lse_sh : (int64_t)0; };
 
   Ctx<D, T> x;
   x.lds = (LDS_AS char*)smem_raw;
@@ -926,8 +934,8 @@ void attn_fwd_kernel(AttnArgs a) {
       mx_lane = slot_body<D, T>(x, scur, snxt, o, l, kb, vbase, settle);
     }
     if (DUAL && (w_cur & kWordLast)) {
-      T* os = static_cast<T*>(a.o_s) + o_base;
-      float* lse_s = a.lse_s ? a.lse_s + lse_base : nullptr;
+      T* os = static_cast<T*>(a.o_s) + o_base + o_dh();
+      float* lse_s = a.lse_s ? a.lse_s + lse_base + lse_dh() : nullptr;
       emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, q_off, lane);
       emitted_s = true;
     }
@@ -944,12 +952,12 @@ void attn_fwd_kernel(AttnArgs a) {
 
   if (wave_valid) {
     if (DUAL && !emitted_s) {
-      T* os = static_cast<T*>(a.o_s) + o_base;
-      float* lse_s = a.lse_s ? a.lse_s + lse_base : nullptr;
+      T* os = static_cast<T*>(a.o_s) + o_base + o_dh();
+      float* lse_s = a.lse_s ? a.lse_s + lse_base + lse_dh() : nullptr;
       emit<D, T>(o, m, l, x.c, os, a.o_st, lse_s, x.qrow, T_, q_off, lane);
     }
-    T* ot = static_cast<T*>(a.o_t) + o_base;
-    float* lse_t = a.lse_t ? a.lse_t + lse_base : nullptr;
+    T* ot = static_cast<T*>(a.o_t) + o_base + o_dh();
+    float* lse_t = a.lse_t ? a.lse_t + lse_base + lse_dh() : nullptr;
     emit<D, T>(o, m, l, x.c, ot, a.o_st, lse_t, x.qrow, T_, q_off, lane);
   }
 }
