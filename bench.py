@@ -104,10 +104,14 @@ def cpu_baseline(q, k, v, cfg, target_s: float) -> dict:
         for W in (wt, ws):
             attn_ref.band_reference(qpad, kc[:, :off + n], vc[:, :off + n], 0, W, rows=rows)
 
+    # Size the sample from a warm 128-row probe (the first call also pays for
+    # thread start-up and allocation), so the four timed-or-warm-up runs take
+    # about target_s together.
+    run(128)
     t0 = time.perf_counter()
-    run(64)
-    t64 = time.perf_counter() - t0
-    n = int(min(span, max(64, round(64 * (target_s / 4) / max(t64, 1e-3) / 64) * 64)))
+    run(128)
+    t128 = time.perf_counter() - t0
+    n = int(min(span, max(64, round(128 * (target_s / 4) / max(t128, 1e-3) / 64) * 64)))
     run(n)  # warm-up
     times = []
     for _ in range(3):
