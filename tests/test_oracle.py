@@ -11,6 +11,7 @@ fail the same checks.
 from __future__ import annotations
 
 import math
+import sys
 import os
 
 import numpy as np
@@ -224,3 +225,19 @@ def test_golden_fixtures():
         assert np.allclose(o.numpy(), z[name], rtol=0, atol=2e-6)
     x, w = to_bf16(z["conv_x"]), to_bf16(z["conv_w"])
     assert np.array_equal(_bits(conv_ref.dwconv_c(x, w)).numpy(), z["conv_y"])
+
+
+def test_golden_attn_fixtures():
+    """tests/golden/golden_attn.npz (the kernels' head sizes) still reproduces: the
+    oracle's fp32 outputs and LSEs."""
+    sys.path.insert(0, GOLDEN)
+    from make_golden import attn_cases
+    z = np.load(os.path.join(GOLDEN, "golden_attn.npz"), allow_pickle=False)
+    to_bf16 = lambda a: torch.from_numpy(a.astype(np.int16)).view(torch.bfloat16)  # noqa: E731
+    for name, *_ in attn_cases():
+        q, k, v = (to_bf16(z[f"{name}_{t}"]) for t in "qkv")
+        wt, ws = (int(w) for w in z[f"{name}_windows"])
+        for which, W in (("teacher", wt), ("student", ws)):
+            o, lse = attn_ref.dense_reference(q, k, v, W, return_lse=True)
+            assert np.allclose(o.numpy(), z[f"{name}_o_{which}"], rtol=0, atol=2e-6)
+            assert np.allclose(lse.numpy(), z[f"{name}_lse_{which}"], rtol=0, atol=2e-6)
