@@ -10,8 +10,9 @@
 // consecutive rows along C: consecutive lanes own consecutive 16-byte
 // chunks, so every row access of a wavefront is one fully coalesced 1 KiB
 // transaction. The K-1 previous rows stay in registers as a sliding window,
-// so x is fetched once per row (plus a K-1 row halo per run, an L2 hit since
-// the neighbouring run streams the same rows). y is written with
+// so x is fetched once per row plus a K-1 row halo per run (the halo misses
+// L2 as often as not: it is requested while the neighbouring run fetches the
+// same rows, so HBM reads are (R + K - 1) / R of x). y is written with
 // non-temporal stores: it is consumed by the next op, not by this kernel.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
