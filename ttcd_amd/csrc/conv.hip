@@ -7,13 +7,15 @@
 //
 // The op is HBM-bound (one read of x, one write of y), so there is no MFMA
 // here. Each thread owns 16 bytes along D (8 bf16 channels) and a run of R
-// consecutive rows along C: consecutive lanes own consecutive 16-byte
-// chunks, so every row access of a wavefront is one fully coalesced 1 KiB
-// transaction. The K-1 previous rows stay in registers as a sliding window,
-// so x is fetched once per row plus a K-1 row halo per run (the halo misses
-// L2 as often as not: it is requested while the neighbouring run fetches the
-// same rows, so HBM reads are (R + K - 1) / R of x). y is written with
-// non-temporal stores: it is consumed by the next op, not by this kernel.
+// consecutive rows along C, and the K-1 previous rows stay in registers as a
+// sliding window. For K <= 8 (dwconv_halo_kernel) a wavefront holds 16
+// groups along D of 4 consecutive runs, and each run's K-1 halo rows come
+// from the run below it through a lane shuffle, so x is read (4R + K - 1) /
+// 4R times. (A halo re-read from memory by every run misses L2 as often as
+// not: it is requested while the neighbouring run fetches the same rows,
+// which cost 25 % more HBM reads at R = 16.) y is written with non-temporal
+// stores: it is consumed by the next op, not by this kernel. Other K, or
+// unaligned tensors, take dwconv_scalar_kernel.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -58,22 +60,38 @@ union Pack16 {
 
 constexpr int kRows = 16;  // rows of C per thread
 
+// Shared-halo layout (K <= kRows + 1): a wavefront owns 16 consecutive
+// 16-byte groups along D (lane % 16) of 4 consecutive runs along C (lane /
+// 16), so each row access is four contiguous 256-byte pieces. The K-1 halo
+// rows of run g are the last rows of run g-1, taken from the lanes 16 below
+// with a lane shuffle; only the first run of a wavefront reads its halo from
+// memory, so x is read (kRows * 4 + K - 1) / (kRows * 4) times instead of
+// (kRows + K - 1) / kRows.
 template <typename X, typename W, int K>
-__global__ __launch_bounds__(256) void dwconv_vec_kernel(const X* __restrict__ x,
-                                                         const W* __restrict__ w,
-                                                         X* __restrict__ y, int64_t N, int C,
-                                                         int D, int nseg) {
+__global__ __launch_bounds__(256) void dwconv_halo_kernel(const X* __restrict__ x,
+                                                          const W* __restrict__ w,
+                                                          X* __restrict__ y, int64_t N, int C,
+                                                          int D, int nseg) {
+  static_assert(K - 1 <= kRows, "the halo must lie within the previous run");
   constexpr int V = Pack16<X>::N;
   const int ngroups = D / V;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = N * nseg * (int64_t)ngroups;
-  if (gid >= total) return;
-  const int dg = (int)(gid % ngroups);
-  const int64_t rest = gid / ngroups;
-  const int seg = (int)(rest % nseg);
-  const int64_t n = rest / nseg;
-  const int d0 = dg * V;
-  const int c0 = seg * kRows;
+  const int ntile = (ngroups + 15) / 16;
+  const int nquad = (nseg + 3) / 4;
+  const int lane = threadIdx.x & 63;
+  // one wavefront per (n, quad of runs, 16-group tile); whole wavefronts leave
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t total = N * nquad * (int64_t)ntile;
+  if (wid >= total) return;
+  const int tile = (int)(wid % ntile);
+  const int64_t rest = wid / ntile;
+  const int quad = (int)(rest % nquad);
+  const int64_t n = rest / nquad;
+  const int g = lane >> 4;
+  const int dg = tile * 16 + (lane & 15);
+  const bool col_ok = dg < ngroups;
+  const int d0 = (col_ok ? dg : 0) * V;  // idle lanes read a valid group, store nothing
+  const int c0 = (quad * 4 + g) * kRows;
+  const int rows = col_ok ? max(0, min(kRows, C - c0)) : 0;
 
   float wr[K][V];
 #pragma unroll
@@ -84,62 +102,49 @@ __global__ __launch_bounds__(256) void dwconv_vec_kernel(const X* __restrict__ x
   const X* xb = x + n * C * (int64_t)D + d0;
   X* yb = y + n * C * (int64_t)D + d0;
 
-  // win[t] holds row c - (K-1) + t for the row c being produced.
+  Pack16<X> in[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    in[r].raw = u32x4{0u, 0u, 0u, 0u};
+    if (r < rows) in[r].raw = *reinterpret_cast<const u32x4*>(xb + (int64_t)(c0 + r) * D);
+  }
+
+  // win[t] holds row c - (K-1) + t for the row c being produced. Every lane
+  // takes part in the shuffles; run g > 0 has a full run g-1 below it.
   float win[K][V];
 #pragma unroll
   for (int t = 0; t < K - 1; ++t) {
-    const int c = c0 - (K - 1) + t;
     Pack16<X> p;
-    p.raw = u32x4{0u, 0u, 0u, 0u};
-    if (c >= 0) p.raw = *reinterpret_cast<const u32x4*>(xb + (int64_t)c * D);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      p.raw[q] = (uint32_t)__shfl_up((int)in[kRows - (K - 1) + t].raw[q], 16, 64);
+    if (g == 0) {
+      const int c = c0 - (K - 1) + t;
+      p.raw = u32x4{0u, 0u, 0u, 0u};
+      if (c >= 0 && rows > 0) p.raw = *reinterpret_cast<const u32x4*>(xb + (int64_t)c * D);
+    }
 #pragma unroll
     for (int e = 0; e < V; ++e) win[t][e] = Cvt<X>::to_f(p.e[e]);
   }
 
-  const int rows = min(kRows, C - c0);
-  if (rows == kRows) {
-    Pack16<X> in[kRows];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r)
-      in[r].raw = *reinterpret_cast<const u32x4*>(xb + (int64_t)(c0 + r) * D);
+  for (int r = 0; r < kRows; ++r) {
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
+    for (int e = 0; e < V; ++e) win[K - 1][e] = Cvt<X>::to_f(in[r].e[e]);
+    Pack16<X> out;
 #pragma unroll
-      for (int e = 0; e < V; ++e) win[K - 1][e] = Cvt<X>::to_f(in[r].e[e]);
-      Pack16<X> out;
+    for (int e = 0; e < V; ++e) {
+      float acc = 0.f;
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < K; ++j) acc = fmaf(win[j][e], wr[j][e], acc);
-        out.e[e] = Cvt<X>::from_f(acc);
-      }
+      for (int j = 0; j < K; ++j) acc = fmaf(win[j][e], wr[j][e], acc);
+      out.e[e] = Cvt<X>::from_f(acc);
+    }
+    if (r < rows)
       __builtin_nontemporal_store(out.raw, reinterpret_cast<u32x4*>(yb + (int64_t)(c0 + r) * D));
 #pragma unroll
-      for (int t = 0; t < K - 1; ++t)
+    for (int t = 0; t < K - 1; ++t)
 #pragma unroll
-        for (int e = 0; e < V; ++e) win[t][e] = win[t + 1][e];
-    }
-  } else {
-    for (int r = 0; r < rows; ++r) {
-      Pack16<X> in;
-      in.raw = *reinterpret_cast<const u32x4*>(xb + (int64_t)(c0 + r) * D);
-#pragma unroll
-      for (int e = 0; e < V; ++e) win[K - 1][e] = Cvt<X>::to_f(in.e[e]);
-      Pack16<X> out;
-#pragma unroll
-      for (int e = 0; e < V; ++e) {
-        float acc = 0.f;
-#pragma unroll
-        for (int j = 0; j < K; ++j) acc = fmaf(win[j][e], wr[j][e], acc);
-        out.e[e] = Cvt<X>::from_f(acc);
-      }
-      *reinterpret_cast<u32x4*>(yb + (int64_t)(c0 + r) * D) = out.raw;
-#pragma unroll
-      for (int t = 0; t < K - 1; ++t)
-#pragma unroll
-        for (int e = 0; e < V; ++e) win[t][e] = win[t + 1][e];
-    }
+      for (int e = 0; e < V; ++e) win[t][e] = win[t + 1][e];
   }
 }
 
@@ -172,9 +177,9 @@ hipError_t launch_vec(const void* x, const void* w, void* y, int64_t N, int C, i
                       hipStream_t st) {
   constexpr int V = Pack16<X>::N;
   const int nseg = (C + kRows - 1) / kRows;
-  const int64_t total = N * nseg * (int64_t)(D / V);
-  const int64_t blocks = (total + 255) / 256;
-  hipLaunchKernelGGL((dwconv_vec_kernel<X, W, K>), dim3((unsigned)blocks), dim3(256), 0, st,
+  const int64_t waves = N * ((nseg + 3) / 4) * (int64_t)((D / V + 15) / 16);
+  const int64_t blocks = (waves * 64 + 255) / 256;
+  hipLaunchKernelGGL((dwconv_halo_kernel<X, W, K>), dim3((unsigned)blocks), dim3(256), 0, st,
                      static_cast<const X*>(x), static_cast<const W*>(w), static_cast<X*>(y), N,
                      C, D, nseg);
   return hipGetLastError();
