@@ -184,6 +184,34 @@ def test_outputs_do_not_depend_on_strides(gpu):
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(4, 2, 128), (6, 2, 64), (3, 1, 128)])
+@torch.inference_mode()
+def test_head_major_views_equal_contiguous(gpu, heads, kv_heads, head_dim):
+    """(B, H, T, D) tensors passed as (B, T, H, D) views (token stride D, head
+    stride T*D) give the same outputs and LSEs, bit for bit, as contiguous
+    inputs: fused call in both rescale modes, single band, LSE variant."""
+    from ttcd_amd import band_attn, fused_dual_window_attn, lse_dual_window_attn
+    g = torch.Generator().manual_seed(heads * head_dim)
+    B, T = 2, 600
+
+    def hm(h):
+        return torch.randn(B, h, T, head_dim, generator=g).to(torch.bfloat16).cuda().transpose(1, 2)
+
+    q, k, v = hm(heads), hm(kv_heads), hm(kv_heads)
+    assert q.stride(1) == head_dim and q.stride(2) == T * head_dim
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    for exact in (False, True):
+        a = fused_dual_window_attn(q, k, v, 300, 129, return_lse=True, exact_max=exact)
+        b = fused_dual_window_attn(qc, kc, vc, 300, 129, return_lse=True, exact_max=exact)
+        assert all(torch.equal(x, y) for x, y in zip(a, b)), ("fused", exact)
+    a = band_attn(q, k, v, 129, 300, return_lse=True)
+    b = band_attn(qc, kc, vc, 129, 300, return_lse=True)
+    assert all(torch.equal(x, y) for x, y in zip(a, b)), "band"
+    a = lse_dual_window_attn(q, k, v, 300, 129)
+    b = lse_dual_window_attn(qc, kc, vc, 300, 129)
+    assert all(torch.equal(x, y) for x, y in zip(a, b)), "LSE variant"
+
+
 @torch.inference_mode()
 def test_runs_on_current_stream(gpu):
     from ttcd_amd import fused_dual_window_attn

@@ -11,7 +11,8 @@ form evaluates any subset of rows at the cost of those rows alone):
   far band's lower edge and its masking run on the GPU
   (profiling/bench_attn_bsz.py:26-40);
 * the LSE-combination variant on the same shapes, since config 4 compares it
-  with the fused kernel.
+  with the fused kernel;
+* a sequence four times the headline length (T=262144) at both head sizes.
 
 Outputs and LSEs are checked on rows around 0, w_S, w_T and the tail, at the
 attention bars of test_attn_gpu.py; size-independent properties (finite
@@ -131,3 +132,23 @@ def test_narrow_gaps_with_active_teacher_boundary(gpu, wt, ws):
     torch.cuda.synchronize()
     rows = torch.cat([torch.arange(wt - 8, T), torch.arange(ws - 16, ws + 16)]).unique()
     _check_sampled(q, k, v, outs, wt, ws, rows, [0], torch.float16)
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(2, 1, 128), (3, 1, 64)])
+@torch.inference_mode()
+def test_long_sequence_256k(gpu, heads, kv_heads, head_dim):
+    """T = 262144, four times the headline length (query blocks, slot words
+    and element offsets at that size), both head sizes, the even (two heads
+    per wavefront) and odd group layouts; rows around 0, w_S, w_T, the
+    middle and the tail against the oracle."""
+    from ttcd_amd import fused_dual_window_attn
+    T, WT, WS = 262144, 8192, 4096
+    print(f"long sequence: T={T} Hq={heads} Hkv={kv_heads} D={head_dim}", flush=True)
+    q, k, v = make_qkv(batch=1, seqlen=T, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
+                       seed=head_dim + heads)
+    outs = fused_dual_window_attn(q, k, v, WT, WS, return_lse=True)
+    torch.cuda.synchronize()
+    assert outs[0].isfinite().all() and outs[1].isfinite().all()
+    assert torch.equal(outs[0][:, :WS], outs[1][:, :WS])
+    rows = _rows(T, WT, WS, extra=(131000, 200003))
+    _check_sampled(q, k, v, outs, WT, WS, rows, [0], torch.bfloat16)
