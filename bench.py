@@ -568,6 +568,10 @@ def main() -> int:
         "pct_bf16_peak": 100 * tflops / PEAK_BF16_TFLOPS,
         "tokens_per_s": B * T / (ms * 1e-3),
         "flops_per_step": F,
+        # secondary line: the work of the two separate calls the fused call
+        # replaces (teacher band + student band), over the same time
+        "two_call_equivalent_flops": F + F_s,
+        "two_call_equivalent_tflops": (F + F_s) / (ms * 1e-3) / 1e12,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": traffic,
                      "traffic_source": traffic_note},
