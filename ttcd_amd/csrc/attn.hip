@@ -323,18 +323,33 @@ __device__ __forceinline__ int key_of(int j0, int kt, int e, int half) {
   return j0 + kt * 32 + 8 * (e >> 2) + 4 * half + (e & 3);
 }
 
-// Mask S^T of the tile at j0 to band b (in place).
+// Mask S^T of the tile at j0 to band b (in place): key j is visible to row
+// qrow iff 0 <= qrow - j - lo < hi - lo and 0 <= j < T. Element (kt, e) of
+// this lane holds key j0 + 4*half + o with o = 32kt + 8(e/4) + e%4 a
+// compile-time constant, so the band test is one unsigned compare of a
+// per-lane value minus o against the uniform width. Keys outside [0, T) can
+// only be in a tile that starts before 0 or runs past T - 1 (a uniform
+// test); only such tiles take the second pass.
 __device__ __forceinline__ void mask_band(f32x16 (&s)[2], int qrow, int j0, int T_, Band b,
                                           int half) {
   const unsigned width = (unsigned)(b.hi - b.lo);
+  const unsigned d = (unsigned)qrow - (unsigned)(j0 + 4 * half) - (unsigned)b.lo;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int j = key_of(j0, kt, e, half);
-      const bool ok = (unsigned)(qrow - j - b.lo) < width && (unsigned)j < (unsigned)T_;
-      s[kt][e] = ok ? s[kt][e] : -INFINITY;
+      const unsigned o = (unsigned)key_of(0, kt, e, 0);
+      s[kt][e] = (d - o) < width ? s[kt][e] : -INFINITY;
     }
+  if (j0 < 0 || j0 + kBlockN > T_) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int j = key_of(j0, kt, e, half);
+        s[kt][e] = (unsigned)j < (unsigned)T_ ? s[kt][e] : -INFINITY;
+      }
+  }
 }
 
 __device__ __forceinline__ float tile_max(const f32x16 (&s)[2]) {
@@ -639,7 +654,7 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
   return reinterpret_cast<const T*>((uint64_t)lo | ((uint64_t)hi << 32));
 }
 
-// Wavefronts per SIMD: two for D = 128 (230 VGPRs); three for D = 64, whose
+// Wavefronts per SIMD: two for D = 128 (<= 256 VGPRs); three for D = 64, whose
 // slots carry half the MFMA work for the same softmax VALU work and need
 // more waves to issue from (<= 168 VGPRs, 3 x 32 KiB of LDS per CU).
 #ifndef TTCD_D64_WAVES
