@@ -222,8 +222,9 @@ ttcd_status ttcd_lse_dual_window_attn_fwd(
  * ttcd_lse_dual_window_attn_fwd. Every call on one GPU shares the array:
  * calls that overlap in time on one GPU (different streams with no ordering
  * between them) race; calls on one stream are safe. The first call on a
- * device resolves the array's address there (hipGetSymbolAddress). Other
- * arguments as in ttcd_lse_dual_window_attn_fwd.
+ * device resolves the array's address there (hipGetSymbolAddress), so make
+ * that first call outside HIP graph capture; later calls can be captured
+ * and replayed. Other arguments as in ttcd_lse_dual_window_attn_fwd.
  */
 size_t ttcd_lse_dual_window_attn_noalloc_scratch_bytes(void);
 ttcd_status ttcd_lse_dual_window_attn_noalloc_fwd(

@@ -2,7 +2,10 @@
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
 this module, as the checker. Everything runs in torch on the CPU in fp32 (or
-fp64 where stated); nothing here touches the GPU.
+fp64 where stated), except band_reference_blocked, which runs plain torch
+fp32 ops on whatever device its inputs live on (the GPU tests give it GPU
+tensors to check every row of the 64K shapes); none of it calls this
+repository's HIP library.
 
 Functions and the reference lines they restate
   dense_reference               - test/test_fused_dual_attn.py:88-110 (fp32
@@ -12,6 +15,8 @@ Functions and the reference lines they restate
   band_reference                - the same math query-chunked over the band
                                   (keys i-hi+1 .. i-lo only), optionally on a
                                   subset of rows; the form used at T = 64K.
+  band_reference_blocked        - the same math again, blocked over all rows
+                                  with torch.matmul (device-agnostic).
   lse_merge_reference           - profiling/lse_dual_attn.py:32-38 / :119-131.
   emulate_reference_kernel      - the block algorithm of _fused_dual_swa_fwd
                                   (profiling/fused_dual_attn.py:56-241): 64-row
@@ -25,7 +30,7 @@ Functions and the reference lines they restate
 Pins (tests/test_oracle.py): brute_force_attention on tiny shapes (an
 implementation with no shared code); closed forms (all-equal scores -> mean
 of V over the window; window 1 -> o = v; window >= T -> plain causal);
-dense == banded; lse == logsumexp identity; merge(student, far band) ==
+dense == banded == blocked; lse == logsumexp identity; merge(student, far band) ==
 teacher; the emulator against dense_reference within bf16 tolerance.
 """
 from __future__ import annotations
@@ -114,6 +119,50 @@ def band_reference(q, k, v, lo: int, hi: int | None, *, rows=None, chunk: int = 
     return (out, lse) if return_lse else out
 
 
+def band_reference_blocked(q, k, v, lo: int, hi: int | None, *, q_block: int = 512,
+                           return_lse: bool = False):
+    """Every row of band_reference's math (Tq == Tk; fp32 masked softmax over the
+    keys i-hi+1 .. i-lo of query i), a block of q_block query rows at a time, on
+    the inputs' own device: contiguous fp32 operands through torch.matmul, the
+    query heads of one K/V head stacked as rows (head h reads K/V head h // G).
+
+    This is the full-size checker: on GPU tensors it evaluates all 65536 rows of
+    the 64K shapes in seconds with torch's own fp32 GEMMs and softmax, a path
+    that shares no code with this repository's HIP library. Returns fp32
+    o (B, T, H, D) (and lse (B, H, T), natural log; -inf and o = 0 for an empty
+    band).
+    """
+    B, T, H, D = q.shape
+    HK = k.shape[2]
+    G = H // HK
+    hi = T if (hi is None or hi < 0) else hi
+    dev = q.device
+    out = torch.zeros(B, T, H, D, dtype=torch.float32, device=dev)
+    lse = torch.full((B, H, T), NEG_INF, dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    for i0 in range(0, T, q_block):
+        i1 = min(T, i0 + q_block)
+        jlo, jhi = max(0, i0 - hi + 1), min(T - 1, i1 - 1 - lo)
+        if jhi < jlo:
+            continue
+        n, m = i1 - i0, jhi - jlo + 1
+        qs = (q[:, i0:i1].float().reshape(B, n, HK, G, D).permute(0, 2, 3, 1, 4)
+              .reshape(B, HK, G * n, D).contiguous())
+        ks_t = k[:, jlo:jhi + 1].float().permute(0, 2, 3, 1).contiguous()  # (B, HK, D, m)
+        vs = v[:, jlo:jhi + 1].float().permute(0, 2, 1, 3).contiguous()    # (B, HK, m, D)
+        s = torch.matmul(qs, ks_t).mul_(scale).view(B, HK, G, n, m)
+        dist = (torch.arange(i0, i1, device=dev)[:, None]
+                - torch.arange(jlo, jhi + 1, device=dev)[None, :])
+        s.masked_fill_(~((dist >= lo) & (dist < hi)), NEG_INF)
+        lc = torch.logsumexp(s, dim=-1)  # (B, HK, G, n)
+        p = torch.softmax(s, dim=-1).nan_to_num_(0.0)
+        del s
+        oc = torch.matmul(p.view(B, HK, G * n, m), vs)  # (B, HK, G*n, D)
+        out[:, i0:i1] = oc.view(B, HK, G, n, D).permute(0, 3, 1, 2, 4).reshape(B, n, H, D)
+        lse[:, :, i0:i1] = lc.reshape(B, H, n)
+    return (out, lse) if return_lse else out
+
+
 def brute_force_attention(q, k, v, lo: int, hi: int):
     """Scalar float64 loops (tiny inputs): o[b,i,h] = sum_j softmax_j(s_ij) v_j over
     lo <= i - j < hi, 0 <= j <= i; returns (o, lse) as float64 tensors."""
@@ -198,11 +247,16 @@ def _reuse_update(ss, mtc, m_t_new, p, pv, c):
 
 
 def emulate_reference_kernel(q, k, v, window_teacher, window_student, *, block_m: int = 64,
-                             block_n: int = 64):
+                             block_n: int = 64, row_blocks=None, heads=None):
     """CPU emulation of the reference Triton kernel's numerics; returns
     (o_teacher, o_student) in q.dtype. Used to report the fraction of GPU
     outputs bit-identical to the reference kernel's algorithm (the last bits
-    still depend on each device's dot-product reduction order and exp2)."""
+    still depend on each device's dot-product reduction order and exp2).
+
+    row_blocks (first rows, multiples of block_m) and heads restrict the
+    emulation to those query blocks and heads, as the kernel computes each
+    (block, head) independently; the other outputs are left as zeros. This
+    samples the 64K shapes, where the whole emulation would take hours."""
     B, T, H, D = q.shape
     HK = k.shape[2]
     G = H // HK
@@ -212,21 +266,23 @@ def emulate_reference_kernel(q, k, v, window_teacher, window_student, *, block_m
     c = float(torch.tensor(D ** -0.5, dtype=torch.float32) * torch.tensor(LOG2E, dtype=torch.float32))
     c = torch.tensor(c, dtype=torch.float32)
     BM, BN = block_m, block_n
-    ot = torch.empty(B, T, H, D, dtype=dt)
-    os_ = torch.empty(B, T, H, D, dtype=dt)
-    qf, kf, vf = q.float(), k.float(), v.float()
+    ot = torch.zeros(B, T, H, D, dtype=dt)
+    os_ = torch.zeros(B, T, H, D, dtype=dt)
+    blocks = range(0, T, BM) if row_blocks is None else [int(r) for r in row_blocks]
+    assert all(r % BM == 0 and 0 <= r < T for r in blocks), "row blocks start at multiples of block_m"
     for b in range(B):
-        for h in range(H):
+        for h in (range(H) if heads is None else heads):
             hk = h // G
             kh = torch.zeros(T + BN, D)
             vh = torch.zeros(T + BN, D)
-            kh[:T] = kf[b, :, hk]
-            vh[:T] = vf[b, :, hk]
-            for m_start in range(0, T, BM):
+            kh[:T] = k[b, :, hk].float()
+            vh[:T] = v[b, :, hk].float()
+            qf = q[b, :, h].float()
+            for m_start in blocks:
                 rows = torch.arange(m_start, m_start + BM)
                 qb = torch.zeros(BM, D)
                 nval = min(BM, T - m_start)
-                qb[:nval] = qf[b, m_start:m_start + nval, h]
+                qb[:nval] = qf[m_start:m_start + nval]
                 st, ss = _State(BM, D), _State(BM, D)
                 m_end = m_start + BM - 1
                 nb_last = m_end // BN

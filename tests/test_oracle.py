@@ -103,6 +103,36 @@ def test_banded_matches_dense(lo, hi, rows):
     assert torch.allclose(rl, dl[:, :, idx], atol=1e-12)
 
 
+@pytest.mark.parametrize("lo,hi,qb", [(0, 37, 16), (10, 50, 7), (0, 200, 64), (0, 1, 33),
+                                      (0, None, 50), (4, 5, 9)])
+def test_blocked_matches_brute_force_and_banded(lo, hi, qb):
+    """band_reference_blocked (the full-row checker of the 64K GPU tests) against the
+    scalar float64 brute force and band_reference, over every row, with blocks that
+    do not divide T and a GQA group of 3 (the head -> K/V head map is exercised)."""
+    T = 130
+    q, k, v = _qkv(T, 6, 2, 16, seed=(hi or T) + lo, dtype=torch.float32, B=2)
+    ho = T if hi is None else hi
+    bo, bl = attn_ref.brute_force_attention(q[:, :60], k[:, :60], v[:, :60], lo, ho)
+    o, lse = attn_ref.band_reference_blocked(q, k, v, lo, hi, q_block=qb, return_lse=True)
+    assert o.dtype == torch.float32 and o.shape == q.shape and lse.shape == (2, 6, T)
+    assert torch.allclose(o[:, :60].double(), bo, atol=2e-6, rtol=0)
+    fin = ~torch.isinf(bl)
+    assert torch.equal(torch.isinf(lse[:, :, :60]), ~fin)
+    assert torch.allclose(lse[:, :, :60].double()[fin], bl[fin], atol=2e-6, rtol=0)
+    ro, rl = attn_ref.band_reference(q, k, v, lo, hi, return_lse=True)
+    assert torch.allclose(o, ro, atol=2e-6, rtol=0)
+    assert torch.allclose(lse[~torch.isinf(rl)], rl[~torch.isinf(rl)], atol=2e-6, rtol=0)
+
+
+def test_blocked_detects_planted_head_map_mistake():
+    """Planted mistake: K/V heads swapped in a copy of the inputs (the wrong GQA map)
+    must move the blocked reference far from the brute force."""
+    q, k, v = _qkv(40, 4, 2, 16, seed=5, dtype=torch.float32)
+    o = attn_ref.band_reference_blocked(q, k.flip(2), v.flip(2), 0, 12, q_block=16)
+    bo, _ = attn_ref.brute_force_attention(q, k, v, 0, 12)
+    assert (o.double() - bo).abs().max().item() > 0.1
+
+
 @pytest.mark.parametrize("ws,wt", [(16, 40), (1, 2), (30, 100)])
 def test_lse_merge_identity(ws, wt):
     """softmax over disjoint bands [0, ws) + [ws, wt) merged by LSE == window wt
@@ -125,6 +155,20 @@ def test_reference_kernel_emulator_within_tolerance():
         for W, o in ((wt, et), (ws, es)):
             mx, mean = attn_ref.error_stats(o, attn_ref.dense_reference(q, k, v, W))
             assert mx <= 2e-2 and mean <= 4e-4, (wt, ws, W, mx, mean)
+
+
+def test_reference_kernel_emulator_sampled_blocks_equal_full_run():
+    """Sampling (row_blocks, heads), as the headline numerics report does, gives the
+    same bits as those blocks of the whole emulation."""
+    q, k, v = _qkv(300, 4, 2, 64, seed=74)
+    ft, fs = attn_ref.emulate_reference_kernel(q, k, v, 256, 128)
+    st, ss = attn_ref.emulate_reference_kernel(q, k, v, 256, 128, row_blocks=[64, 256],
+                                               heads=[1, 2])
+    for r0, r1 in ((64, 128), (256, 300)):
+        for h in (1, 2):
+            assert torch.equal(st[:, r0:r1, h], ft[:, r0:r1, h])
+            assert torch.equal(ss[:, r0:r1, h], fs[:, r0:r1, h])
+    assert not st[:, :64].any() and not st[:, :, 0].any()
 
 
 def test_ulp_report_known_values():

@@ -79,3 +79,44 @@ def test_noalloc_matches_workspace_entry_two_calls(gpu):
             got = o[b:b + 1, rows].float().cpu()
             err = (got - ref.float()).abs()
             assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3, (i, hi, err.max())
+
+
+def _launch(q, k, v, ot, os_, wt, ws):
+    """The allocation-free call on torch's current stream, no synchronisation (so it
+    can be captured)."""
+    from ttcd_amd import _lib
+    L = _lib.lib()
+    B, T, H, D = q.shape
+    dt = _lib.DTYPE_BF16 if q.dtype == torch.bfloat16 else _lib.DTYPE_F16
+    _lib.check(L.ttcd_lse_dual_window_attn_noalloc_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), ot.data_ptr(), os_.data_ptr(), B, T, T, H,
+        k.shape[2], D, _lib.strides4(q.stride()), _lib.strides4(k.stride()),
+        _lib.strides4(v.stride()), _lib.strides4(ot.stride()), wt, ws, D ** -0.5, 8.0, dt,
+        torch.cuda.current_stream().cuda_stream))
+
+
+@torch.inference_mode()
+def test_noalloc_replays_under_graph_capture(gpu):
+    """Captured in a HIP graph after one eager call on the device (which resolves the
+    scratch address; the header asks for that call before any capture), three replays
+    on new inputs, eager work and synchronisations between them, each bit-identical to
+    the workspace entry point on the same inputs."""
+    B, T, H, HK, D, wt, ws = 1, 3000, 8, 4, 128, 1500, 700
+    q, k, v = _inputs(B, T, H, HK, D, torch.bfloat16, seed=21, dev=gpu)
+    ot, os_ = torch.empty_like(q), torch.empty_like(q)
+    _launch(q, k, v, ot, os_, wt, ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _launch(q, k, v, ot, os_, wt, ws)
+    g = torch.Generator(device=gpu)
+    for rep in range(3):
+        g.manual_seed(200 + rep)
+        for t in (q, k, v):
+            t.copy_(torch.randn(t.shape, generator=g, device=gpu).to(t.dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        got_t, got_s = ot.clone(), os_.clone()
+        want_t, want_s = _call(q, k, v, wt, ws, noalloc=False)
+        assert torch.equal(got_t, want_t), f"replay {rep}: teacher"
+        assert torch.equal(got_s, want_s), f"replay {rep}: student"
