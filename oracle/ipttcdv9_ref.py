@@ -24,7 +24,9 @@ rounding its result to the model dtype where the reference stores it:
                         170-270): RMSNorm, q|k|v projections, q/k RMSNorm +
                         rotary, windowed causal attention (attn_ref.
                         band_reference), o_proj, residual RMSNorm, SwiGLU MLP
-                        or the TTT MLP, final norm, LM head.
+                        or the TTT MLP, final norm, LM head; optionally one
+                        chunk of a prompt prefilled over a K/V cache
+                        (new_cache_ref).
 
 Pins (tests/test_ipttcdv9.py): ttt_mlp_scan_ref in float64 == ttt_mlp_token_f64
 (two formulations: chunk GEMMs + grouped cumsum vs per-token outer products),
@@ -33,8 +35,12 @@ for one and several groups and a ragged last chunk; a planted off-by-one
 features reduce to the plain MLP z @ W_down^T; swiglu_ref against
 x * sigmoid(x) * y in float64 within one rounding; prefill_ref with no TTT
 layers and window >= T equals a dense causal transformer written with
-dense_reference; the components it composes are pinned in their own test
-files (attention, rotary, RMSNorm, conv).
+dense_reference; a prompt prefilled in chunks over the cache, with no TTT
+layers (whose MLP restarts per chunk), gives the one-shot prefill's logits,
+also when the cache has been trimmed to the window, and a planted mistake
+(a rotary offset that does not continue) does not; the components it
+composes are pinned in their own test files (attention, rotary, RMSNorm,
+conv).
 """
 from __future__ import annotations
 
@@ -221,8 +227,26 @@ def output_gate_ref(c: dict, w: dict, p: str, x, o, dt):
     return (on.double() * act.to(dt).double()).to(dt).reshape(B, T, -1)
 
 
+def new_cache_ref() -> dict:
+    """An empty K/V cache for prefill_ref's chunked prefill: the tokens seen and,
+    per layer, the rotated keys and the values kept for the next chunk."""
+    return {"seen": 0, "kv": {}}
+
+
+def _cached_band(q, k_all, v_all, W):
+    """Attention of the last Tq positions of a Tk-token sequence (bottom-right
+    aligned, window W): band_reference over the full length with the queries
+    placed at the end (earlier rows zero and not evaluated)."""
+    B, Tq, H, D = q.shape
+    Tk = k_all.shape[1]
+    qpad = torch.zeros(B, Tk, H, D, dtype=q.dtype)
+    qpad[:, Tk - Tq:] = q
+    return attn_ref.band_reference(qpad, k_all, v_all, 0, W, rows=torch.arange(Tk - Tq, Tk))
+
+
 def prefill_ref(cfg: dict, w: dict, input_ids: torch.Tensor, logits_to_keep: int = 1,
-                dt=torch.bfloat16, attention_mask=None, cu_seqlens=None) -> torch.Tensor:
+                dt=torch.bfloat16, attention_mask=None, cu_seqlens=None,
+                cache: dict | None = None) -> torch.Tensor:
     """Logits (B, logits_to_keep, V) of the reference prefill on the CPU.
     cfg: a resolved config (ttcd_amd.ipttcdv9.resolve_config); w: the
     parameters under the reference's state-dict names (CPU tensors).
@@ -234,18 +258,29 @@ def prefill_ref(cfg: dict, w: dict, input_ids: torch.Tensor, logits_to_keep: int
     sequence, with rotary positions restarting per packed sequence (not
     shifted for padding: a prefill has no cache). The TTT student is
     flash_attn_func on the whole padded / packed rows (:825-827), and the TTT
-    MLP runs on them as they are. Padded rows attend nowhere: o = 0."""
+    MLP runs on them as they are. Padded rows attend nowhere: o = 0.
+
+    cache (new_cache_ref(), then the same dict for every later chunk): a
+    prefill in chunks over a K/V cache. Rotary positions continue from
+    cache["seen"]; every layer's attention (teacher window, and the student
+    window on TTT layers) runs over the kept keys of the earlier chunks
+    followed by the chunk's own, the queries at the end (the flash_attn_func
+    calls on the cached k / v of modeling_ipttcdv9.py:741-751, 771-787 and
+    fla/layers/attn.py:215-226); each layer then keeps the last window_size
+    of them (every key with no window), enough that the next chunk's first
+    query sees its whole window; the TTT MLP sees the chunk alone."""
     c = cfg
     B, T = input_ids.shape
     H, I, D = c["hidden_size"], c["intermediate_size"], c["head_dim"]
     Hq, Hkv = c["num_heads"], c["num_kv_heads"]
     eps = c["norm_eps"]
-    rows_tab = max(T, c["max_position_embeddings"] or 0)
+    off = 0 if cache is None else cache["seen"]
+    rows_tab = max(off + T, c["max_position_embeddings"] or 0)
     inv = prologue_ref.inv_freq_ref(D, c["rope_theta"])
     cos, sin = prologue_ref.tables_ref(inv, rows_tab, dt)
-    pos = _positions(T, cu_seqlens)
+    pos = _positions(T, cu_seqlens) + off
     cos, sin = cos[pos], sin[pos]
-    Wt = c["window_size"] if c["window_size"] is not None else T
+    Wt = c["window_size"] if c["window_size"] is not None else off + T
     Ws = c["ttt_visible_chunks"] * c["ttt_chunk"]
     if attention_mask is not None and bool(attention_mask.all()):
         attention_mask = None
@@ -254,6 +289,8 @@ def prefill_ref(cfg: dict, w: dict, input_ids: torch.Tensor, logits_to_keep: int
         return prologue_ref.rms_norm_ref(x, wt, eps)
 
     def attn(q, k, v, W):
+        if k.shape[1] > q.shape[1]:
+            return _cached_band(q, k, v, W).to(dt)
         return attn_ref.band_reference(q, k, v, 0, W).to(dt)
 
     def teacher_attn(q, k, v):
@@ -290,6 +327,12 @@ def prefill_ref(cfg: dict, w: dict, input_ids: torch.Tensor, logits_to_keep: int
             q = prologue_ref.rms_norm_ref(q, w[p + "attn.q_norm.weight"], 1e-5)
             k = prologue_ref.rms_norm_ref(k, w[p + "attn.k_norm.weight"], 1e-5)
         q, k = _rope(q, cos, sin), _rope(k, cos, sin)
+        if cache is not None:
+            old = cache["kv"].get(i)
+            if old is not None:
+                k, v = torch.cat([old[0], k], 1), torch.cat([old[1], v], 1)
+            n = k.shape[1] if c["window_size"] is None else min(c["window_size"], k.shape[1])
+            cache["kv"][i] = (k[:, k.shape[1] - n:], v[:, v.shape[1] - n:])
         o_w = w[p + "attn.o_proj.weight"]
         ttt = i in c["ttt_layers"] and T >= c["ttt_chunk"]
         a_t = _mm(gated(p, x, teacher_attn(q, k, v)), o_w.t(), dt)
@@ -305,6 +348,8 @@ def prefill_ref(cfg: dict, w: dict, input_ids: torch.Tensor, logits_to_keep: int
             up = _mm(x, w[p + "mlp.up_proj.weight"].t(), dt)
             y = _mm(swiglu_ref(gate, up), w[p + "mlp.down_proj.weight"].t(), dt)
         h = (residual.float() + y.float()).to(dt)
+    if cache is not None:
+        cache["seen"] += T
     keep = h[:, -logits_to_keep:] if logits_to_keep > 0 else h
     x = norm(keep, w["model.norm.weight"])
     return _mm(x, w["lm_head.weight"].t(), dt)

@@ -331,3 +331,43 @@ def test_oracle_padding_mask_equals_unpadded_row_up_to_rope_positions():
     masked = R.prefill_ref(c, w, ids, 0, torch.float32, attention_mask=mask)
     alone = R.prefill_ref(c, w, ids[:, :50], 0, torch.float32)
     torch.testing.assert_close(masked[:, :50], alone, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("window,chunks", [(64, (100, 60, 40)), (None, (70, 50)),
+                                           (64, (30, 20, 110))])
+def test_oracle_chunked_prefill_equals_one_shot(window, chunks):
+    """A prompt prefilled in chunks over the oracle's K/V cache gives every row
+    the logits of one prefill of the whole prompt, on a TTT-free config (the TTT
+    MLP restarts per chunk): the rotary offset continues, each chunk attends
+    over the kept keys, and a cache trimmed to the window (first case) still
+    holds every key the next chunk's window reaches."""
+    cfg = dict(TINY, ttt_layers=[], num_hidden_layers=2, window_size=window)
+    c = M.resolve_config(cfg)
+    w = M.init_weights(cfg, "cpu", seed=6)
+    T = sum(chunks)
+    ids = torch.randint(0, 1024, (2, T), generator=torch.Generator().manual_seed(7))
+    whole = R.prefill_ref(c, w, ids, 0, torch.float32)
+    cache = R.new_cache_ref()
+    a = 0
+    for n in chunks:
+        part = R.prefill_ref(c, w, ids[:, a:a + n], 0, torch.float32, cache=cache)
+        torch.testing.assert_close(part, whole[:, a:a + n], rtol=1e-4, atol=1e-4)
+        a += n
+        assert cache["seen"] == a
+        kept = cache["kv"][0][0].shape[1]
+        assert kept == (a if window is None else min(window, a))
+
+
+def test_oracle_chunked_prefill_detects_planted_offset_mistake():
+    """Planted mistake: the second chunk's rotary positions restart at 0 (the
+    cache's token count dropped) -- its logits must move off the one-shot ones."""
+    cfg = dict(TINY, ttt_layers=[], num_hidden_layers=2, window_size=64)
+    c = M.resolve_config(cfg)
+    w = M.init_weights(cfg, "cpu", seed=6)
+    ids = torch.randint(0, 1024, (1, 120), generator=torch.Generator().manual_seed(8))
+    whole = R.prefill_ref(c, w, ids, 0, torch.float32)
+    cache = R.new_cache_ref()
+    R.prefill_ref(c, w, ids[:, :80], 0, torch.float32, cache=cache)
+    cache["seen"] = 0
+    bad = R.prefill_ref(c, w, ids[:, 80:], 0, torch.float32, cache=cache)
+    assert (bad - whole[:, 80:]).abs().max().item() > 1e-2

@@ -396,3 +396,47 @@ def test_output_gate_on_every_path_matches_oracle(gate_fn):
     plain = R.prefill_ref(dict(c, use_output_gate=False), {k: v.cpu() for k, v in w.items()},
                           ids, 8, torch.bfloat16)
     assert (plain.float() - want.float()).abs().mean() > 0.1 * want.float().abs().mean()
+
+
+@pytest.mark.parametrize("chunks", [(600, 300), (300, 700, 256)])
+def test_prefill_in_chunks_over_the_cache_matches_oracle(chunks):
+    """A prompt prefilled in chunks over IPTTCDv9Cache (the attention kernels'
+    Tq < Tk forms, the window-trimmed per-layer K/V, the rotary offset) against
+    the oracle's chunked prefill, every path. Every chunk has at least one TTT
+    chunk (256 tokens), so the TTT layers run the dual-window kernel on
+    Tq < Tk; (600, 300): the first chunk already fills the 512-token window,
+    so the cache is trimmed before the second; (300, 700, 256): the cache
+    grows, then is trimmed, and the last chunk is exactly one TTT chunk."""
+    c = M.resolve_config(TINY)
+    w = M.init_weights(TINY, DEV, seed=9)
+    wc = {k: v.cpu() for k, v in w.items()}
+    T = sum(chunks)
+    ids = torch.randint(0, c["vocab_size"], (1, T), generator=torch.Generator().manual_seed(T))
+    for p in M.PATHS:
+        model = M.IPTTCDv9Prefill(TINY, w, path=p)
+        cache, rcache = M.IPTTCDv9Cache(), R.new_cache_ref()
+        a = 0
+        for n in chunks:
+            print(f"path {p}: chunk {a}..{a + n}", flush=True)
+            got = model.forward(ids[:, a:a + n].to(DEV), logits_to_keep=8, cache=cache)
+            torch.cuda.synchronize()
+            want = R.prefill_ref(c, wc, ids[:, a:a + n], 8, torch.bfloat16, cache=rcache)
+            _logits_close(got, want)
+            a += n
+            assert cache.seen == a
+            assert cache.kv[0][0].shape[1] == min(a, TINY["window_size"])
+
+
+def test_prefill_in_chunks_equals_one_prefill_without_ttt():
+    """With no TTT layer (the TTT MLP restarts per chunk), a chunked prefill's
+    logits equal one prefill of the whole prompt on every row."""
+    cfg = dict(TINY, ttt_layers=[])
+    w = M.init_weights(cfg, DEV, seed=10)
+    model = M.IPTTCDv9Prefill(cfg, w)
+    ids = _ids(1, 1000, seed=11).to(DEV)
+    whole = model.forward(ids, logits_to_keep=0)
+    cache, a = M.IPTTCDv9Cache(), 0
+    for n in (450, 50, 500):
+        part = model.forward(ids[:, a:a + n], logits_to_keep=0, cache=cache)
+        _logits_close(part, whole[:, a:a + n], max_frac=2e-2, mean_frac=1e-2)
+        a += n

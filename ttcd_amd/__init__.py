@@ -15,8 +15,8 @@ bare-module drop-in used by patches.py):
     dual_residual_rmsnorm / fused_attn_epilogue (attention epilogue: one o_proj
     GEMM over both outputs, then both residual RMSNorms in one pass); rmsnorm
     swiglu / swiglu_mlp / ttt_features / ttt_mlp (the MLPs, ttcd_amd.ttt)
-    IPTTCDv9Prefill / init_weights (the ipttcdv9 prefill end to end,
-    ttcd_amd.ipttcdv9)
+    IPTTCDv9Prefill / IPTTCDv9Cache / init_weights (the ipttcdv9 prefill end
+    to end, optionally in chunks over a K/V cache, ttcd_amd.ipttcdv9)
 """
 from .attn import (band_attn, band_attn_varlen, fused_dual_window_attn,
                    fused_dual_window_attn_varlen, lse_dual_window_attn,
@@ -24,7 +24,7 @@ from .attn import (band_attn, band_attn_varlen, fused_dual_window_attn,
                    window_attn)
 from .conv import causal_dwconv_chunked, causal_dwconv_x
 from .epilogue import dual_residual_rmsnorm, fused_attn_epilogue, rmsnorm
-from .ipttcdv9 import IPTTCDv9Prefill, init_weights
+from .ipttcdv9 import IPTTCDv9Cache, IPTTCDv9Prefill, init_weights
 from .prologue import fused_qk_norm_rope, qk_norm_rope, rope_inv_freq, rope_tables
 from .ttt import swiglu, swiglu_mlp, ttt_features, ttt_mlp
 
@@ -33,5 +33,6 @@ __all__ = [
     "lse_dual_window_attn", "lse_dual_window_attn_fa3", "lse_dual_window_attn_fa3_fast",
     "lse_merge", "window_attn", "fused_qk_norm_rope", "qk_norm_rope", "rope_inv_freq",
     "rope_tables", "dual_residual_rmsnorm", "fused_attn_epilogue", "rmsnorm", "swiglu",
-    "swiglu_mlp", "ttt_features", "ttt_mlp", "IPTTCDv9Prefill", "init_weights",
+    "swiglu_mlp", "ttt_features", "ttt_mlp", "IPTTCDv9Prefill", "IPTTCDv9Cache",
+    "init_weights",
 ]

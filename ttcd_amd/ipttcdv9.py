@@ -50,10 +50,29 @@ applied to both attention outputs on every path, including the patched one,
 where the reference's patch drops it (a strict xfail,
 test/test_fused_dual_attn.py:339-360).
 
+Prefill onto a populated cache (`cache=IPTTCDv9Cache()`, forward called once
+per prompt chunk): each layer keeps the last window_size rotated keys and
+values of the tokens already prefilled (all of them for a full-causal model),
+fla's window-trimmed attn_state (fla/models/utils.py:35-96), and the next
+chunk's queries attend over those keys followed by their own, bottom-right
+aligned, through the kernels' Tq < Tk forms (the teacher and, on TTT layers,
+the student window; the reference's unpatched fast path does the same with
+flash_attn_func on the cached k / v, modeling_ipttcdv9.py:741-751, and its
+patched forward falls back to it, profiling/patches.py:270-284). Rotary
+positions continue from the tokens already seen. The TTT MLP sees the chunk's
+tokens only, as the reference's MLP does. Two deliberate departures, both so
+that a chunked prefill attends exactly as one prefill of the whole prompt:
+fla's cache rolls a full cache by the chunk length (the first queries of a
+later chunk then see fewer than window_size keys); here the kept keys always
+reach window_size back from the chunk's first token. And fla's FLACache counts
+the chunk's tokens at layer 0, so layers 1.. read a rotary offset one chunk
+too far (fla/models/utils.py:316-317, 342-345); here every layer uses the
+tokens seen before the chunk.
+
 Not covered (raise NotImplementedError): qkv_bias, non-causal TTT conv,
 ttt_weight_renorm, Muon, normalised TTT features or proj-diff,
-ttt_output_use_teacher_conv, l2 softmax, a KV cache (prefill only; the
-reference's cache writes are copies of k and v).
+ttt_output_use_teacher_conv, l2 softmax, a cache together with a padding
+mask or packed sequences.
 """
 from __future__ import annotations
 
@@ -266,6 +285,8 @@ class IPTTCDv9Prefill:
         self.window_s = c["ttt_visible_chunks"] * c["ttt_chunk"]
 
     def tables(self, T: int):
+        """Rotary cos / sin tables of at least T rows (the reference's cache
+        length, extended when a cached prefill reaches past it)."""
         rows = max(T, self.cfg["max_position_embeddings"] or 0)
         if self._tables is None or self._tables[0].shape[0] < rows:
             self._tables = _pro.rope_tables(self._inv_freq, rows, self.dtype)
@@ -282,11 +303,11 @@ class IPTTCDv9Prefill:
         k = qkv[..., Hq * D:(Hq + Hkv) * D].view(B, T, Hkv, D)
         v = qkv[..., (Hq + Hkv) * D:].view(B, T, Hkv, D)
         p = f"model.layers.{i}.attn."
-        cos, sin = ctx.tables if ctx.tables is not None else self.tables(T)
+        cos, sin = ctx.tables if ctx.tables is not None else self.tables(ctx.offset + T)
         qw = w.get(p + "q_norm.weight") if c["qk_norm"] else None
         kw = w.get(p + "k_norm.weight") if c["qk_norm"] else None
         # fla's RMSNorm default eps for q_norm / k_norm (fla/layers/attn.py:61-63)
-        q, k = _pro.qk_norm_rope(q, k, qw, kw, 1e-5, cos, sin, 0)
+        q, k = _pro.qk_norm_rope(q, k, qw, kw, 1e-5, cos, sin, ctx.offset)
         return q, k, v
 
     @property
@@ -340,6 +361,8 @@ class IPTTCDv9Prefill:
         return on * act
 
     def _ttt_attention(self, q, k, v):
+        """Teacher and student outputs of a TTT layer; k / v may be longer than q
+        (a cached prefill: the queries are the last positions)."""
         if self.attn_kernel == "triton":
             return _attn.fused_dual_window_attn(q, k, v, self.window_t, self.window_s)
         if self.attn_kernel == "fa3_lse":
@@ -364,6 +387,9 @@ class IPTTCDv9Prefill:
             x, residual = _epi.add_rmsnorm(y_prev, h, w[p + "attn_norm.weight"], eps)
         xa = x  # attn_norm output: the gate's input
         q, k, v = self._qkv(i, x, ctx)
+        if ctx.cache is not None:
+            # the cached keys of earlier chunks, then this chunk's (Tk >= T)
+            k, v = ctx.cache.extend(i, k, v, None if self.window_t < 0 else self.window_t)
         o_w = w[p + "attn.o_proj.weight"]
         gated = c["use_output_gate"]
         if i in self.ttt and T >= c["ttt_chunk"]:
@@ -397,11 +423,23 @@ class IPTTCDv9Prefill:
             y = _ttt.swiglu_mlp(x, self.gu_w[i], w[p + "mlp.down_proj.weight"])
         return residual, y
 
-    def _prefill_context(self, B: int, T: int, attention_mask, cu_seqlens) -> "_Prefill":
+    def _prefill_context(self, B: int, T: int, attention_mask, cu_seqlens,
+                         cache: "IPTTCDv9Cache | None" = None) -> "_Prefill":
         """_use_fast_prefill_path (modeling_ipttcdv9.py:562-574) and what the
         fallback needs: unpad indices and cu_seqlens for a padding mask,
-        per-sequence rotary tables for packed sequences."""
+        per-sequence rotary tables for packed sequences; the rotary offset and
+        the cache of a cached prefill."""
         ctx = _Prefill()
+        if cache is not None:
+            if not isinstance(cache, IPTTCDv9Cache):
+                raise ValueError("cache must be an IPTTCDv9Cache")
+            if cu_seqlens is not None or (attention_mask is not None
+                                          and not bool(attention_mask.to(self.dev).bool().all())):
+                raise NotImplementedError("a cached prefill with a padding mask or packed "
+                                          "sequences")
+            cache.check(B, self.Hkv, self.D, self.dtype, self.dev)
+            ctx.cache, ctx.offset = cache, cache.seen
+            attention_mask = None
         if attention_mask is not None:
             if attention_mask.shape != (B, T):
                 raise ValueError(f"attention_mask must be (B, T) = ({B}, {T}), got "
@@ -436,20 +474,25 @@ class IPTTCDv9Prefill:
     @torch.inference_mode()
     def forward(self, input_ids: torch.Tensor, logits_to_keep: int = 1,
                 attention_mask: torch.Tensor | None = None,
-                cu_seqlens: torch.Tensor | None = None) -> torch.Tensor:
+                cu_seqlens: torch.Tensor | None = None,
+                cache: "IPTTCDv9Cache | None" = None) -> torch.Tensor:
         """Logits (B, logits_to_keep, vocab) of the prefill of `input_ids`
         (B, T), as IPTTCDForCausalLM(input_ids, logits_to_keep=...) returns them
         with fuse_linear_cross_entropy off (bench_prefill.py:73-74).
         attention_mask: the (B, T) 0/1 padding mask; cu_seqlens: packed
-        sequences of a (1, T) batch (int32, 0 .. T)."""
+        sequences of a (1, T) batch (int32, 0 .. T); cache: an IPTTCDv9Cache
+        holding the earlier chunks of the prompt (empty for the first), which
+        this call extends with its T tokens."""
         if input_ids.dim() != 2 or input_ids.device != self.dev:
             raise ValueError("input_ids must be (B, T) on the model's device")
         B, T = input_ids.shape
-        ctx = self._prefill_context(B, T, attention_mask, cu_seqlens)
+        ctx = self._prefill_context(B, T, attention_mask, cu_seqlens, cache)
         h = F.embedding(input_ids, self.w["model.embeddings.weight"])
         y = None
         for i in range(self.cfg["num_hidden_layers"]):
             h, y = self.layer(i, h, y, ctx)
+        if cache is not None:
+            cache.seen += T
         if logits_to_keep > 0:  # only the kept rows of the last block's output
             h, y = h[:, -logits_to_keep:], y[:, -logits_to_keep:]
         keep = h + y
@@ -475,6 +518,38 @@ def patch_triton_conv(model: IPTTCDv9Prefill) -> int:
     return len(model.ttt)
 
 
+class IPTTCDv9Cache:
+    """The K/V cache of a prefill in chunks: per layer the rotated keys and the
+    values of the last `window_size` tokens already prefilled (all of them
+    when the model attends full-causally), fla's window-trimmed attn_state
+    (fla/models/utils.py:35-96), and the count of tokens seen. Pass the same
+    object to every IPTTCDv9Prefill.forward of one prompt."""
+
+    def __init__(self):
+        self.seen = 0
+        self.kv: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+        self._shape = None
+
+    def check(self, B: int, Hkv: int, D: int, dtype, device) -> None:
+        shape = (B, Hkv, D, dtype, torch.device(device))
+        if self._shape is not None and self._shape != shape:
+            raise ValueError(f"cache holds (B, Hkv, D, dtype, device) = {self._shape}, "
+                             f"this prefill needs {shape}")
+        self._shape = shape
+
+    def extend(self, layer: int, k: torch.Tensor, v: torch.Tensor, keep: int | None):
+        """Keys / values for layer's attention: the cached ones, then k / v of
+        this chunk (B, T, Hkv, D). Keeps the last `keep` of them (all with None)
+        for the next chunk."""
+        old = self.kv.get(layer)
+        if old is not None:
+            k = torch.cat([old[0], k], 1)
+            v = torch.cat([old[1], v], 1)
+        n = k.shape[1] if keep is None else min(keep, k.shape[1])
+        self.kv[layer] = (k[:, k.shape[1] - n:].contiguous(), v[:, v.shape[1] - n:].contiguous())
+        return k, v
+
+
 class _Prefill:
     """Per-forward state of the fast-path gate and the fallback."""
 
@@ -484,6 +559,8 @@ class _Prefill:
         self.cu_seqlens = None    # int32 sequence starts (unpadded rows or packed)
         self.max_seqlen = 0
         self.tables = None        # per-token rotary rows for packed sequences
+        self.cache = None         # IPTTCDv9Cache of a cached prefill
+        self.offset = 0           # rotary offset: tokens prefilled before this call
 
 
 class _NormView:
