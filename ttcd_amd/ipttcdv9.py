@@ -66,7 +66,7 @@ fla's cache rolls a full cache by the chunk length (the first queries of a
 later chunk then see fewer than window_size keys); here the kept keys always
 reach window_size back from the chunk's first token. And fla's FLACache counts
 the chunk's tokens at layer 0, so layers 1.. read a rotary offset one chunk
-too far (fla/models/utils.py:316-317, 342-345); here every layer uses the
+too far (fla/models/utils.py:326-327, 349-352); here every layer uses the
 tokens seen before the chunk.
 
 Not covered (raise NotImplementedError): qkv_bias, non-causal TTT conv,
