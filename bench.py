@@ -17,7 +17,8 @@ the chunked causal conv at the reference's benchmark shape (GB/s vs 8 TB/s),
 the attention prologue (q/k RMSNorm + rotary) and epilogue (o_proj + dual
 residual RMSNorm) on the same layer, the reference's other 64K window recipes
 (2048/1024 and 16384/8192), the fused outputs against the single-band kernel
-on every row (bit-equal fraction), the batch / narrow-gap sweep (fused vs
+on every row (bit-equal fraction), full causal attention against torch's SDPA
+flash backend on the same tensors, the batch / narrow-gap sweep (fused vs
 LSE variant), the ipttcdv9 prefill end to end (28 layers, T=32768; fused,
 patched and stock paths; and T=65536, the length of the reference's published
 end-to-end numbers), numerics at the CPU-runnable config and on sampled query
@@ -220,6 +221,42 @@ def recipes_measure(q, k, v, steps: int = 10, warmup: int = 3) -> list:
                     "reference_h100_ms": {"fused": r["ref_h100_fused_ms"],
                                           "two_calls": r["ref_h100_two_calls_ms"],
                                           "source": "profiling/REPORT.md:252-253"}})
+    return out
+
+
+def vendor_sdpa_measure(q, k, v, steps: int = 5, warmup: int = 2) -> dict:
+    """The vendor attention on this box as a yardstick: torch's
+    scaled_dot_product_attention with its flash backend (AOTriton on ROCm) on
+    full causal attention over the headline tensors, against this library's
+    single-band kernel on the same problem (window = T). PyTorch has no sliding
+    window, so full causal is the problem both can run; the FLOPs are equal.
+    SDPA gets contiguous (B, H, T, D) copies made outside the timed region."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from ttcd_amd import window_attn, work as W
+
+    B, T, H, D = q.shape
+    HK = k.shape[2]
+    F = W.attn_flops(B, H, D, T, None)
+    ms_own = time_gpu(lambda: window_attn(q, k, v, None), steps, warmup)
+    o_own = window_attn(q, k, v, None)
+    qh, kh, vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(  # noqa: E731
+        qh, kh, vh, is_causal=True, enable_gqa=HK != H)
+    out = {"problem": f"full causal, B={B} T={T} Hq={H} Hkv={HK} D={D}, bf16", "flops": F,
+           "own_ms": ms_own, "own_tflops": F / (ms_own * 1e-3) / 1e12,
+           "torch_version": torch.__version__}
+    try:
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            o_v = sdpa()
+            ms_v = time_gpu(sdpa, steps, warmup)
+        out.update({"sdpa_backend": "flash", "sdpa_ms": ms_v,
+                    "sdpa_tflops": F / (ms_v * 1e-3) / 1e12, "own_speedup": ms_v / ms_own,
+                    "max_abs_diff": (o_v.transpose(1, 2).float() - o_own.float()).abs().max().item()})
+        del o_v
+    except RuntimeError as e:  # no flash kernel for this build / shape
+        out.update({"sdpa_backend": None, "sdpa_error": str(e)[:200]})
+    log(f"vendor SDPA yardstick: {out}")
     return out
 
 
@@ -639,6 +676,7 @@ def main() -> int:
                 res["recipes_64k"] = recipes_measure(q, k, v)
                 res["second_kernel_agreement"] = second_kernel_agreement(q, k, v, wt, ws)
                 log(f"fused vs single-band kernel, every row: {res['second_kernel_agreement']}")
+                res["vendor_sdpa_full_causal"] = vendor_sdpa_measure(q, k, v)
                 res["smollm2"] = second_shape_measure("smollm2")
             res["config4_sweep"] = sweep_measure()
             res["e2e_prefill"] = e2e_measure()
