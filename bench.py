@@ -369,7 +369,21 @@ def profile_one(args) -> int:
         k = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
         v = torch.randn(B, T, HK, D, device=dev, dtype=torch.bfloat16, generator=gen)
         work, unit = W.attn_flops(B, H, D, T, wt), "TFLOP/s"
-        if args.only == "fused":
+        if args.only in ("causal", "sdpa"):
+            # full causal: this library's single-band kernel, or torch's SDPA
+            # flash backend on contiguous (B, H, T, D) copies
+            work = W.attn_flops(B, H, D, T, None)
+            if args.only == "causal":
+                fn = lambda: window_attn(q, k, v, None)  # noqa: E731
+            else:
+                from torch.nn.attention import SDPBackend, sdpa_kernel
+                qh, kh, vh = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+
+                def fn():
+                    with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+                        return torch.nn.functional.scaled_dot_product_attention(
+                            qh, kh, vh, is_causal=True, enable_gqa=HK != H)
+        elif args.only == "fused":
             fn = lambda: fused_dual_window_attn(q, k, v, wt, ws, return_lse=True)  # noqa: E731
         elif args.only == "band":
             fn = lambda: window_attn(q, k, v, wt)  # noqa: E731
@@ -581,8 +595,8 @@ def main() -> int:
     ap.add_argument("--no-numerics", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seqlen", type=int, default=32768, help="prompt length of --only e2e")
-    ap.add_argument("--only", choices=["fused", "band", "lse", "conv", "copy", "prologue",
-                                       "epilogue", "sweep", "e2e"],
+    ap.add_argument("--only", choices=["fused", "band", "lse", "causal", "sdpa", "conv", "copy",
+                                       "prologue", "epilogue", "sweep", "e2e"],
                     help="profiling mode: run one workload --steps times and print its timing")
     args = ap.parse_args()
 
