@@ -529,9 +529,10 @@ __device__ __forceinline__ float slot_body(const Ctx<D, T>& x, f32x16 (&sc)[2], 
 }
 
 // Scores of a slot exp'd under the previous slot's PV MFMAs in the lazy mode
-// (the rest run under the slot's own score MFMAs).
+// (the rest run under the slot's own score MFMAs). Half and half measured
+// fastest at D = 128: 8, 12, 20 and 24 (24 spills) were 0.3-1.9 % slower.
 #ifndef TTCD_EA
-#define TTCD_EA 8
+#define TTCD_EA 16
 #endif
 template <int D>
 constexpr int lazy_ea() {
