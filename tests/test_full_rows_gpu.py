@@ -5,7 +5,8 @@ lse_teacher and lse_student on all rows, not samples.
 
 * config 2, the headline: T=65536, Hq=16, Hkv=8, D=128, (8192, 4096), bf16
   and fp16, the fused call in both rescale modes and the LSE variant;
-* config 3, SmolLM2-360M's layer: Hq=15, Hkv=5, D=64;
+* config 3, SmolLM2-360M's layer: Hq=15, Hkv=5, D=64, bf16 and fp16;
+* full causal attention (window None) at T=16384, both head sizes;
 * config 4: B = 1, 2, 4, 8 at T=16384, and the narrow gaps (8192, 7168) /
   (8192, 8064) at T=32768 (profiling/bench_attn_bsz.py:26-40);
 * the reference's other published 64K recipes, (2048, 1024) and
@@ -114,20 +115,40 @@ def test_headline_every_row(gpu, dtype):
     _check_rows(os_, rs[0], dtype, "LSE variant student")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @torch.inference_mode()
-def test_config3_smollm2_every_row(gpu):
+def test_config3_smollm2_every_row(gpu, dtype):
     from ttcd_amd import fused_dual_window_attn, lse_dual_window_attn
     T, WT, WS = 65536, 8192, 4096
-    print("config 3 every row: SmolLM2 T=65536 Hq=15 Hkv=5 D=64 (8192, 4096)", flush=True)
-    q, k, v = make_qkv(batch=1, seqlen=T, heads=15, kv_heads=5, head_dim=64, seed=3)
+    print(f"config 3 every row: SmolLM2 T=65536 Hq=15 Hkv=5 D=64 (8192, 4096) {dtype}",
+          flush=True)
+    q, k, v = make_qkv(batch=1, seqlen=T, heads=15, kv_heads=5, head_dim=64, seed=3,
+                       dtype=dtype)
     rt, rs = _refs(q, k, v, WT, WS)
     for exact in (False, True):
         outs = fused_dual_window_attn(q, k, v, WT, WS, return_lse=True, exact_max=exact)
-        _check_fused(outs, rt, rs, torch.bfloat16, "fused " + ("exact" if exact else "lazy"))
+        _check_fused(outs, rt, rs, dtype, "fused " + ("exact" if exact else "lazy"))
         del outs
     ot, os_ = lse_dual_window_attn(q, k, v, WT, WS)
-    _check_rows(ot, rt[0], torch.bfloat16, "LSE variant teacher")
-    _check_rows(os_, rs[0], torch.bfloat16, "LSE variant student")
+    _check_rows(ot, rt[0], dtype, "LSE variant teacher")
+    _check_rows(os_, rs[0], dtype, "LSE variant student")
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(16, 8, 128), (15, 5, 64)])
+@torch.inference_mode()
+def test_full_causal_every_row(gpu, heads, kv_heads, head_dim):
+    """Full causal attention (window None: the longest sweeps, up to 256 tiles
+    per workgroup at T = 16384) on every row: the single-band call, and the
+    fused call with a full-causal teacher and a 4096 student."""
+    from ttcd_amd import fused_dual_window_attn, window_attn
+    T, WS = 16384, 4096
+    print(f"full causal every row: T={T} Hq={heads} Hkv={kv_heads} D={head_dim}", flush=True)
+    q, k, v = make_qkv(batch=1, seqlen=T, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
+                       seed=head_dim + 7)
+    rt, rs = _refs(q, k, v, T, WS)
+    _check_rows(window_attn(q, k, v, None), rt[0], torch.bfloat16, "single band, full causal")
+    outs = fused_dual_window_attn(q, k, v, None, WS, return_lse=True)
+    _check_fused(outs, rt, rs, torch.bfloat16, f"fused (full, {WS})")
 
 
 @pytest.mark.parametrize("B", [1, 2, 4, 8])
