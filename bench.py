@@ -21,8 +21,9 @@ on every row (bit-equal fraction), full causal attention against torch's SDPA
 flash backend on the same tensors, the batch / narrow-gap sweep (fused vs
 LSE variant), the ipttcdv9 prefill end to end (28 layers, T=32768; fused,
 patched and stock paths; and T=65536, the length of the reference's published
-end-to-end numbers), numerics at the CPU-runnable config and on sampled query
-blocks of the headline shape, and the CPU baseline: the fp32 masked
+end-to-end numbers, in one call and in four 16K chunks over the K/V cache),
+numerics at the CPU-runnable config and on sampled query blocks of the
+headline shape, and the CPU baseline: the fp32 masked
 softmax of the reference's CPU path (oracle restatement), query-chunked over
 the band, on a bounded sample of rows, on this host's cores.
 """
@@ -502,6 +503,36 @@ def e2e_measure(steps: int = 5, warmup: int = 2, T: int = E2E_T,
     return out
 
 
+def e2e_chunked_measure(T: int = 65536, chunk: int = 16384, steps: int = 3,
+                        warmup: int = 1) -> dict:
+    """The same prefill (fused path, same weights and token ids as
+    e2e_measure) in chunks over the K/V cache: T tokens as T / chunk calls of
+    IPTTCDv9Prefill.forward sharing one IPTTCDv9Cache, so every attention
+    call after the first runs Tq = chunk queries against the cached window.
+    Timed over the whole prompt; logits of the last token."""
+    import torch
+    from ttcd_amd import ipttcdv9
+
+    dev = torch.device("cuda:0")
+    cfg = ipttcdv9.QWEN3_06B_SWA8K
+    weights = ipttcdv9.init_weights(cfg, dev, seed=0)
+    g = torch.Generator(device=dev).manual_seed(1234)
+    ids = torch.randint(0, cfg["vocab_size"], (1, T), device=dev, generator=g)
+    model = ipttcdv9.IPTTCDv9Prefill(cfg, weights, path="fused")
+
+    def run():
+        cache = ipttcdv9.IPTTCDv9Cache()
+        for c0 in range(0, T, chunk):
+            logits = model.forward(ids[:, c0:c0 + chunk], logits_to_keep=1, cache=cache)
+        return logits
+
+    with torch.inference_mode():
+        ms = time_gpu(run, steps, warmup)
+    log(f"e2e prefill T={T} in chunks of {chunk} over the cache: {ms:.2f} ms")
+    return {"T": T, "chunk": chunk, "calls": -(-T // chunk), "path": "fused", "ms": ms,
+            "tokens_per_s": T / (ms * 1e-3)}
+
+
 def epilogue_measure(o_t, o_s, cfg) -> dict:
     """The attention epilogue on the fused kernel's outputs: the dual residual
     RMSNorm alone (HBM-bound, GB/s against 8 TB/s), and the whole drop-in (one
@@ -701,6 +732,10 @@ def main() -> int:
                 "hardware": "one H100 80GB", "source": "profiling/REPORT.md:25, :321",
                 "note": "other hardware and the reference's generate() prefill; context only"}
             res["e2e_prefill_64k"] = e64
+            e64c = e2e_chunked_measure()
+            e64c["one_shot_fused_ms"] = e64["fused"]["ms"]
+            e64c["vs_one_shot"] = e64["fused"]["ms"] / e64c["ms"]
+            res["e2e_prefill_64k_chunked"] = e64c
     # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE / WRITE_SIZE) on
     # the build whose attention sources hash to `attn_sources_sha256`; dropped
     # (null) when the sources timed here differ
