@@ -25,7 +25,10 @@
 // rounded and normalised from its rounded value, as the two launches do.
 //
 // One wavefront per row: lane l owns the 16-byte chunks l, l + 64, ... of
-// the row, so every access is a coalesced 1 KiB transaction.
+// the row, so every access is a coalesced 1 KiB transaction. All of a lane's
+// loads (activations and weight chunks) are issued before the first is used:
+// with a load per chunk behind its own bounds branch, the compiler waited for
+// each chunk before issuing the next (3.8 % slower at hidden 1024).
 // Activations are read once, with non-temporal loads; the weight row, shared
 // by every row, and the outputs, read by the next layer, stay cached.
 #include <hip/hip_runtime.h>
@@ -77,23 +80,38 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(
 
   float xt[MAXC][8], xs[MAXC][8];
   float sst = 0.f, sss = 0.f;
+  // every chunk's loads are issued before the first is used
+  // (a lane past the row's end loads the row's last chunk and uses zeros: no
+  // branch around the loads, so none of them waits for another)
+  V8<T> vt[MAXC], vs[MAXC], vr[MAXC];
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
     const int ch = lane + 64 * c;
-    V8<T> vt, vs, vr;
-    vt.raw = vs.raw = vr.raw = u32x4{0u, 0u, 0u, 0u};
-    if (ch < nch) {
-      vt.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a_t + base + 8 * ch));
-      if (DUAL) vs.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a_s + base + 8 * ch));
-      if (RES) vr.raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(res + base + 8 * ch));
+    const int64_t off = base + 8 * (ch < nch ? ch : nch - 1);
+    vt[c].raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a_t + off));
+    if (DUAL) vs[c].raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a_s + off));
+    if (RES) vr[c].raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(res + off));
+  }
+  // the weight chunks too (shared by every row: cached loads)
+  V8<W> vw[MAXC];
+  if (sizeof(W) == 2) {
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const int ch = lane + 64 * c;
+      vw[c].raw = *reinterpret_cast<const u32x4*>(w + 8 * (ch < nch ? ch : nch - 1));
     }
+  }
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int ch = lane + 64 * c;
+    if (ch >= nch) vt[c].raw = vs[c].raw = vr[c].raw = u32x4{0u, 0u, 0u, 0u};
     V8<T> ro;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float r = RES ? static_cast<float>(vr.e[e]) : 0.f;
-      xt[c][e] = RES ? static_cast<float>(vt.e[e]) + r : static_cast<float>(vt.e[e]);
+      const float r = RES ? static_cast<float>(vr[c].e[e]) : 0.f;
+      xt[c][e] = RES ? static_cast<float>(vt[c].e[e]) + r : static_cast<float>(vt[c].e[e]);
       if (RND) xt[c][e] = static_cast<float>(round_to<T>(xt[c][e]));
-      if (DUAL) xs[c][e] = static_cast<float>(vs.e[e]) + r;
+      if (DUAL) xs[c][e] = static_cast<float>(vs[c].e[e]) + r;
       if (RES) ro.e[e] = round_to<T>(xt[c][e]);
       sst = fmaf(xt[c][e], xt[c][e], sst);
       if (DUAL) sss = fmaf(xs[c][e], xs[c][e], sss);
@@ -110,10 +128,8 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(
     if (ch >= nch) break;
     float wf[8];
     if (sizeof(W) == 2) {
-      V8<W> vw;
-      vw.raw = *reinterpret_cast<const u32x4*>(w + 8 * ch);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) wf[e] = static_cast<float>(vw.e[e]);
+      for (int e = 0; e < 8; ++e) wf[e] = static_cast<float>(vw[c].e[e]);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) wf[e] = static_cast<float>(w[8 * ch + e]);
